@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Expert-FFN decode benchmark on one MI355X (BASELINE.json metric).
+
+Workload (default, configs[1] = C2): GPT-OSS-20B-shape 24-layer MoE expert stack
+(hidden 2880, 32 MXFP4 experts per layer, top-4, intermediate 2880), batch-1
+decode. One step = one token through all 24 layers (router -> top-k -> gate/up
++ SwiGLU -> down + weighted combine per layer), layer-serial in stream order.
+Weights are synthetic (seeded, generated on the GPU), all resident in HBM.
+
+Prints ONE JSON line. `value` is tokens/s over the K timed steps (inputs already
+resident in HBM). `roofline` is the dominant kernel's algorithmic bytes per
+launch over its average launch duration, measured with HIP events on the
+library's stream. `cpu_baseline` times the CPU oracle (the C restatement of the
+reference's CPU path) on a bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "moe-stream_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "valu", "mfma"])
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-tokens", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(layers, specs, n_layers_sample: int, n_tokens_sample: int, threads: int):
+    """Oracle (C restatement of the reference CPU path) on a bounded sample."""
+    import oracle  # test infrastructure; used here only as the timed CPU baseline
+    from moe_rocm import workloads as W
+
+    t_total, n_lt = 0.0, 0
+    for li in range(n_layers_sample):
+        dl, spec = layers[li], specs[li]
+        host = dict(spec=spec)
+        host.update(dl.download_quant())
+        host.update(W.float_tensors(spec))
+        L = oracle.layer_from_host(host)
+        x = W.x_tokens(spec, n_tokens_sample)
+        L.forward(x[:1], n_threads=threads)  # warm-up
+        t0 = time.perf_counter()
+        for t in range(n_tokens_sample):
+            L.forward(x[t:t + 1], n_threads=threads)
+        t_total += time.perf_counter() - t0
+        n_lt += n_tokens_sample
+        del host, L
+    return n_lt / t_total  # layer-tokens per second
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the MoE path is measured on "
+                          "one MI355X; multi-GPU expert parallelism is a design note, not a run",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    import moe_rocm as M
+    from moe_rocm import workloads as W
+
+    ctx = M.Context(0)
+    if a.kernel != "auto":
+        ctx.set_option(M.OPT_DECODE_KERNEL, {"valu": M.DECODE_VALU, "mfma": M.DECODE_MFMA}[a.kernel])
+    specs = W.config_layers(a.config)
+    if a.config == 5:
+        log("config 5 is the batched path; use tests/bench_batched via --config 5 in a later build")
+    n_layers = len(specs)
+    K, Wm = a.steps, a.warmup
+    n_tok = K + Wm
+    t0 = time.perf_counter()
+    layers = [W.DeviceLayer(ctx, s) for s in specs]
+    for dl in layers:
+        dl.layer.reserve(1)
+    log(f"built {n_layers} layers in {time.perf_counter() - t0:.1f}s")
+    H = specs[0].hidden
+    # inputs: x[token][layer] resident in HBM before the timed region
+    xs = np.empty((n_tok, n_layers, H), dtype=np.float32)
+    for li, s in enumerate(specs):
+        xs[:, li, :] = W.x_tokens(s, n_tok)
+    d_x = ctx.to_device(xs)
+    d_y = ctx.zeros((n_layers, H))
+    ctx.sync()
+    xb, yb = d_x.ptr, d_y.ptr
+
+    def enqueue_token(t):
+        for li, dl in enumerate(layers):
+            dl.layer.forward(xb + ((t * n_layers + li) * H) * 4, yb + li * H * 4)
+
+    graphs = []
+    if not a.no_graph:
+        t0 = time.perf_counter()
+        for t in range(n_tok):
+            ctx.graph_begin()
+            enqueue_token(t)
+            graphs.append(ctx.graph_end())
+        log(f"captured {len(graphs)} token graphs in {time.perf_counter() - t0:.1f}s")
+
+    def run(t):
+        if graphs:
+            graphs[t].launch()
+        else:
+            enqueue_token(t)
+
+    for t in range(Wm):
+        run(t)
+    ctx.sync()
+    wall0 = time.perf_counter()
+    ctx.timer_start()
+    for t in range(Wm, n_tok):
+        run(t)
+    ms = ctx.timer_stop()
+    wall = time.perf_counter() - wall0
+    tok_s = K / (ms / 1e3)
+    y = d_y.download(np.float32)
+    assert np.all(np.isfinite(y)), "non-finite output"
+    log(f"timed {K} tokens: {ms:.2f} ms (event), {wall * 1e3:.2f} ms (wall) -> {tok_s:.1f} tok/s")
+
+    bytes_per_token = sum(s.weight_bytes_per_token() for s in specs)
+    flops_per_token = sum(s.flops_per_token() for s in specs)
+
+    # live per-kernel timing (HIP events around each launch, eager, same stream)
+    ctx.set_option(M.OPT_PROFILE, 1)
+    ctx.profile_reset()
+    P = min(a.profile_tokens, n_tok)
+    for t in range(P):
+        enqueue_token(t)
+    ctx.sync()
+    kern = {}
+    for name in ("fused_layer", "gateup", "down", "router_logits", "topk", "shared_gateup"):
+        n, tot = ctx.profile_read(name)
+        if n:
+            kern[name] = (n, tot)
+    ctx.set_option(M.OPT_PROFILE, 0)
+    dom = max(kern, key=lambda k: kern[k][1])
+    n_dom, tot_dom = kern[dom]
+    avg_ms = tot_dom / n_dom
+    s0 = specs[0]
+    t = s0.ggml_type
+    mb = lambda r, c: M.synth.matrix_bytes(t, r, c)  # noqa: E731
+    if dom == "fused_layer":
+        per_launch = sum(s.weight_bytes_per_token() for s in specs) / n_layers
+    elif dom == "gateup":
+        per_launch = s0.top_k * (2 * mb(s0.inter, s0.hidden) + (2 * s0.inter * 4 if s0.expert_bias else 0)) + s0.hidden * 4
+    elif dom == "down":
+        per_launch = s0.top_k * (mb(s0.hidden, s0.inter) + (s0.hidden * 4 if s0.expert_bias else 0)) + s0.hidden * 4
+    else:
+        per_launch = s0.n_experts * s0.hidden * 4
+    achieved = per_launch / (avg_ms * 1e-3) / 1e9
+    log("kernels: " + ", ".join(f"{k}: n={v[0]} avg={v[1] / v[0] * 1e3:.2f}us" for k, v in kern.items()))
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
+        nls, nts = (2, 24) if s0.mxfp4 else (2, 8)
+        t0 = time.perf_counter()
+        lt_s = cpu_baseline(layers, specs, min(nls, n_layers), nts, threads)
+        log(f"cpu baseline: {lt_s:.1f} layer-tok/s in {time.perf_counter() - t0:.1f}s")
+        cpu = {"value": lt_s / n_layers, "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on "
+                         f"{min(nls, n_layers)} of {n_layers} layers x {nts} tokens; "
+                         f"tokens/s = layer-tokens/s / {n_layers}"}
+
+    out = {
+        "metric": "expert-FFN decode tokens/s + achieved HBM GB/s (% peak), GPT-OSS-20B shape",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": round(ms / K, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4-weights/f32" if s0.mxfp4 else "q4_k-weights/f32",
+        "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1))",
+        "config": {"workload": W.CONFIG_NAMES[a.config], "config_id": a.config,
+                   "layers": n_layers, "tokens": K, "hidden": s0.hidden, "inter": s0.inter,
+                   "experts": [s.n_experts for s in specs][:1] if a.config != 4 else "256..512",
+                   "top_k": s0.top_k, "graph": not a.no_graph, "kernel": a.kernel},
+        "hbm_gbs": round(tok_s * bytes_per_token / 1e9, 1),
+        "hbm_frac": round(tok_s * bytes_per_token / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_token": bytes_per_token,
+        "tflops": round(tok_s * flops_per_token / 1e12, 3),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": int(per_launch),
+                     "avg_launch_us": round(avg_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    for g in graphs:
+        g.close()
+    for dl in layers:
+        dl.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

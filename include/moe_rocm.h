@@ -1,0 +1,213 @@
+/*
+ * moe_rocm.h -- C ABI of the MI355X (gfx950) MoE expert-FFN engine.
+ *
+ * Drop-in replacement for the expert-compute backend of moe-stream-core
+ * (GOBA-AI-Labs/moe-stream), which today is the #[cfg(feature="metal")] module
+ * crate::metal (moe-stream-core/src/lib.rs:7-8). Every entry point below names
+ * the reference interface it replaces (path:line relative to
+ * moe-stream-core/src/). Plain C: bindgen-clean, no C++ or HIP types.
+ *
+ * Conventions
+ *  - Every function returns MR_OK (0) or a negative MR_E_* status. No
+ *    exceptions or aborts cross the ABI. mr_last_error(ctx) describes the last
+ *    failing call on that context (replaces candle_core::Error::Msg, e.g.
+ *    metal/mod.rs:1308-1318).
+ *  - Device pointers (`const float* x`, ...) are addresses in the context
+ *    device's global memory, allocated with mr_dev_alloc or by any other HIP
+ *    allocator on that device. Host pointers are marked `host_` and are only
+ *    borrowed for the duration of the call.
+ *  - All device work of a context is enqueued on that context's stream, in
+ *    call order (the reference's single Metal command buffer,
+ *    metal/mod.rs:6-14). Results are visible to the host after mr_sync or a
+ *    download. Scratch buffers are owned by the context and reused by the
+ *    next call (reference: BatchedMoeBuffers, metal/mod.rs:1222-1283), so
+ *    calls on one context must not run concurrently from several host threads.
+ *  - mr_moe_forward / mr_moe_forward_batched launch no allocation and no
+ *    memset; with scratch reserved up front they may be captured into a HIP
+ *    graph (mr_graph_* below).
+ */
+#ifndef MOE_ROCM_H
+#define MOE_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define MR_OK 0
+#define MR_E_INVAL (-1)       /* bad argument or shape */
+#define MR_E_NOMEM (-2)       /* device allocation failed */
+#define MR_E_NODEV (-3)       /* no HIP device, or a host-only context */
+#define MR_E_LAUNCH (-4)      /* kernel launch or HIP runtime failure */
+#define MR_E_UNSUPPORTED (-5) /* valid request outside what this build runs */
+
+/* ---- GGML block types (reader.rs:34-128) --------------------------------- */
+#define MR_GGML_Q4_K 12  /* 144-byte super-block of 256 elements */
+#define MR_GGML_MXFP4 39 /* 17-byte block: e8m0 scale + 32 e2m1 codes */
+
+/* ---- routing flags (top_k_routing, layer.rs:2346-2403) ------------------- */
+/* GPT-OSS: top-k on raw logits, softmax over the k (softmax_weight=true). */
+#define MR_ROUTE_SOFTMAX_AFTER_TOPK 1u
+/* standard mode: renormalise the k probabilities (norm_topk_prob, config.rs:364). */
+#define MR_ROUTE_NORM_TOPK 2u
+
+/* ---- activations (ops/activation.rs:13-38) ----------------------------------- */
+#define MR_ACT_SILU 0        /* silu(g) * u                                   */
+#define MR_ACT_SWIGLU_OAI 1  /* min(g,L)*sigmoid(alpha*min(g,L))*(clamp(u,-L,L)+1) */
+
+/* Device id for a host-only context: argument validation runs, device work
+ * returns MR_E_NODEV. Lets every ABI/error test run without a GPU. */
+#define MR_DEVICE_NONE (-1)
+
+/* Kernel family used by the decode path (mr_ctx_set_option MR_OPT_DECODE_KERNEL). */
+#define MR_OPT_DECODE_KERNEL 1
+#define MR_DECODE_AUTO 0   /* fastest available */
+#define MR_DECODE_VALU 1   /* vector-ALU dequant-matvec kernels, one launch per step */
+#define MR_DECODE_MFMA 2   /* scaled MX-fp4 MFMA matvec, single fused launch per layer */
+/* 1: record a HIP event pair around every kernel launch (read with mr_profile_read). */
+#define MR_OPT_PROFILE 2
+
+typedef struct mr_ctx mr_ctx;
+typedef struct mr_pack mr_pack;
+typedef struct mr_layer mr_layer;
+typedef struct mr_graph mr_graph;
+
+/* ---- context, errors, streams -------------------------------------------- */
+/* Replaces candle's Device::new_metal(0) handle (engine.rs:278-298). */
+int mr_ctx_create(int device, mr_ctx** out);
+void mr_ctx_destroy(mr_ctx* ctx);
+const char* mr_last_error(const mr_ctx* ctx);
+const char* mr_status_string(int status);
+int mr_ctx_device(const mr_ctx* ctx);
+/* Use a caller-owned hipStream_t (cast to void*) instead of the context's own. */
+int mr_ctx_set_stream(mr_ctx* ctx, void* hip_stream);
+void* mr_ctx_stream(const mr_ctx* ctx);
+int mr_ctx_set_option(mr_ctx* ctx, int option, int value);
+/* Wait for all work enqueued on the context stream (the reference syncs at
+ * to_vec1 readbacks, layer.rs:938, engine.rs:2069). */
+int mr_sync(mr_ctx* ctx);
+
+/* ---- device memory ------------------------------------------------------- */
+int mr_dev_alloc(mr_ctx* ctx, uint64_t nbytes, void** out_dptr);
+int mr_dev_free(mr_ctx* ctx, void* dptr);
+/* Stream-ordered copies; both return after the copy has completed. */
+int mr_upload(mr_ctx* ctx, void* dst, const void* host_src, uint64_t nbytes);
+int mr_download(mr_ctx* ctx, void* host_dst, const void* src, uint64_t nbytes);
+/* Enqueue a zero fill with a kernel (graph-capture safe, no memset node). */
+int mr_dev_zero(mr_ctx* ctx, void* dst, uint64_t nbytes);
+
+/* ---- expert weights in native GGUF layout --------------------------------- */
+/* One projection (gate, up or down) of all experts of one layer: E matrices of
+ * [out_features, in_features], expert e starting at host_offsets[e] bytes from
+ * the buffer start (NULL = contiguous, e * bytes_per_expert, the layout of a
+ * stacked ffn_*_exps tensor, reader.rs:394-444). The bytes stay in their
+ * native block layout; nothing is repacked.
+ * mr_pack_upload copies host bytes into a new device buffer the pack owns
+ * (replaces upload_mxfp4_weights, metal/mod.rs:1823, and the packing loop of
+ * preload_experts_gpu, engine.rs:1114-1148). */
+int mr_pack_upload(mr_ctx* ctx, int ggml_type, const void* host_bytes, uint64_t nbytes,
+                   uint32_t n_experts, uint32_t out_features, uint32_t in_features,
+                   const uint64_t* host_offsets, mr_pack** out);
+/* Same over device bytes the caller owns and keeps alive (zero copy; the
+ * reference's Mxfp4Packed views, cache.rs:289-308). */
+int mr_pack_wrap(mr_ctx* ctx, int ggml_type, const void* dev_bytes, uint64_t nbytes,
+                 uint32_t n_experts, uint32_t out_features, uint32_t in_features,
+                 const uint64_t* host_offsets, mr_pack** out);
+void mr_pack_destroy(mr_pack* pack);
+/* Bytes of one [rows, cols] matrix of a GGML block type (reader.rs:99-127). */
+uint64_t mr_matrix_bytes(int ggml_type, uint64_t rows, uint64_t cols);
+/* Dequantize expert `expert` of a pack to f32 [out_features, in_features]
+ * (dequantize_mxfp4 dequant.rs:605, dequantize_q4k dequant.rs:218; the
+ * arithmetic is bit-identical: no contraction). */
+int mr_dequant(mr_ctx* ctx, const mr_pack* pack, uint32_t expert, float* out);
+
+/* ---- one MoE layer ------------------------------------------------------- */
+/* Bundles what run_moe reads for one layer (ResidentWeights fields,
+ * cache.rs:319-398; GpuRoutingOffsets, metal/mod.rs:1440-1485;
+ * ExpertBiasBuffers, metal/mod.rs:1202-1216). Device arrays are borrowed. */
+typedef struct mr_layer_desc {
+  const mr_pack* gate;        /* routed experts: [E, I, H] */
+  const mr_pack* up;          /* [E, I, H] */
+  const mr_pack* down;        /* [E, H, I] */
+  const float* gate_bias;     /* [E, I] f32 or NULL (ffn_gate_exps.bias) */
+  const float* up_bias;       /* [E, I] f32 or NULL */
+  const float* down_bias;     /* [E, H] f32 or NULL */
+  const float* router_w;      /* [E, H] f32 (ffn_gate_inp.weight) */
+  const float* router_b;      /* [E] f32 or NULL (ffn_gate_inp.bias) */
+  const float* dummy_mask;    /* [E] f32, 0 or -inf, or NULL (engine.rs:628-652) */
+  /* optional always-on shared expert (layer.rs:1898-1953): NULL sh_gate disables */
+  const mr_pack* sh_gate;     /* [1, Ish, H] */
+  const mr_pack* sh_up;       /* [1, Ish, H] */
+  const mr_pack* sh_down;     /* [1, H, Ish] */
+  const float* sh_gate_inp;   /* [H] f32 or NULL (ffn_gate_inp_shexp.weight) */
+  uint32_t top_k;             /* 1..16 */
+  uint32_t route_flags;       /* MR_ROUTE_* */
+  uint32_t act;               /* MR_ACT_* for the routed experts (shared expert: SiLU) */
+  float alpha;                /* OAI SwiGLU alpha (1.702, layer.rs:873) */
+  float limit;                /* OAI SwiGLU limit (7.0, layer.rs:874) */
+} mr_layer_desc;
+
+int mr_layer_create(mr_ctx* ctx, const mr_layer_desc* desc, mr_layer** out);
+void mr_layer_destroy(mr_layer* layer);
+/* Allocate context scratch for up to max_tokens tokens of this layer's shape
+ * (BatchedMoeBuffers::new, metal/mod.rs:1240). Call before graph capture. */
+int mr_reserve(mr_ctx* ctx, const mr_layer* layer, uint32_t max_tokens);
+
+/* ---- hot path -------------------------------------------------------------- */
+/* Kernel (1): router GEMV + bias + dummy mask + softmax/top-k for n_tokens
+ * tokens (layer.rs:806-837 + 1012-1027; softmax_topk_kernel,
+ * fused_ops.metal:131-316). idx [T,k] i32, w [T,k] f32, logits [T,E] or NULL. */
+int mr_router_topk(mr_ctx* ctx, const mr_layer* layer, const float* x, uint32_t n_tokens,
+                   int32_t* idx, float* w, float* logits);
+/* Top-k only, over given logits [T,E] (top_k_routing, layer.rs:2346-2403). */
+int mr_topk(mr_ctx* ctx, const float* logits, uint32_t n_tokens, uint32_t n_experts,
+            uint32_t top_k, uint32_t route_flags, int32_t* idx, float* w);
+/* Kernels (2)+(3) with routing given: per token, gate+up dequant-matvec with
+ * bias and SwiGLU, then down dequant-matvec with bias and the weighted combine
+ * in ascending expert order, then the shared expert. y [T,H] is overwritten.
+ * Replaces batched_moe_forward_metal (metal/mod.rs:1297-1435). */
+int mr_moe_experts(mr_ctx* ctx, const mr_layer* layer, const float* x, uint32_t n_tokens,
+                   const int32_t* idx, const float* w, float* y);
+/* Whole layer for one decode token: router, top-k, experts, combine, shared
+ * expert; no host synchronisation. Replaces gpu_routed_moe_forward_metal
+ * (metal/mod.rs:1512-1677) and the CPU run_moe path (layer.rs:756-1980). */
+int mr_moe_forward(mr_ctx* ctx, const mr_layer* layer, const float* x, float* y);
+/* Whole layer for n_tokens tokens (prefill / batched): tokens are grouped by
+ * expert and each expert's weights are read once for all its tokens.
+ * Replaces the multi-token paths layer.rs:1449-1514 and 2148-2183. */
+int mr_moe_forward_batched(mr_ctx* ctx, const mr_layer* layer, const float* x,
+                           uint32_t n_tokens, float* y);
+
+/* ---- graph capture of a sequence of calls (no reference counterpart: the
+ * reference's Metal command buffer batching, metal/mod.rs:6-14) ----------- */
+int mr_graph_begin(mr_ctx* ctx);
+int mr_graph_end(mr_ctx* ctx, mr_graph** out);
+int mr_graph_launch(mr_ctx* ctx, const mr_graph* graph);
+void mr_graph_destroy(mr_graph* graph);
+
+/* ---- timing on the context stream (bench support) ------------------------- */
+/* Records an event pair around the work enqueued between the two calls and
+ * returns the elapsed milliseconds after synchronising. */
+int mr_timer_start(mr_ctx* ctx);
+int mr_timer_stop(mr_ctx* ctx, float* out_ms);
+/* With MR_OPT_PROFILE on: synchronise, then report how many launches of the
+ * named kernel were recorded and their summed duration (ms). Kernel names:
+ * "router_logits", "topk", "gateup", "down", "shared_gateup", "dequant",
+ * "fused_layer", "grouped_gateup", "grouped_down", "group_tokens". */
+int mr_profile_read(mr_ctx* ctx, const char* kernel, uint64_t* out_count, double* out_total_ms);
+int mr_profile_reset(mr_ctx* ctx);
+
+/* ---- synthetic inputs (bench/test support, not a reference interface) ------ */
+/* Fill device bytes with the counter-based SplitMix64 generator of
+ * moe_rocm/synth.py: MXFP4 blocks (e8m0 uniform in [119,127], nibbles uniform)
+ * or Q4_K super-blocks (fp16 d ~|N(0,0.01)|, dmin ~|N(0,0.005)| by the
+ * Irwin-Hall(12) construction, scale and quant bytes uniform). */
+int mr_synth_blocks(mr_ctx* ctx, int ggml_type, void* dst, uint64_t n_blocks, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_ROCM_H */

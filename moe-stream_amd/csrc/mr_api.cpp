@@ -1,0 +1,702 @@
+// mr_api.cpp -- C ABI of include/moe_rocm.h: contexts, device memory, expert
+// packs, layers, argument validation and dispatch to the gfx950 kernels.
+//
+// Every entry point validates its arguments before touching the device, so a
+// host-only context (MR_DEVICE_NONE) exercises every error path without a GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <algorithm>
+#include <new>
+
+#include "mr_internal.h"
+
+namespace {
+
+thread_local std::string g_err;  // errors of calls that have no context
+
+int set_err(mr_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (c)
+    c->err = buf;
+  else
+    g_err = buf;
+  return code;
+}
+
+int hip_fail(mr_ctx* c, hipError_t e, const char* what) {
+  int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? MR_E_NOMEM : MR_E_LAUNCH;
+  return set_err(c, code, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool has_dev(const mr_ctx* c) { return c && c->device >= 0; }
+
+// Make the context's device current for this host thread.
+int bind(mr_ctx* c) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return set_err(c, MR_E_LAUNCH, "hipGetDevice failed");
+  if (cur != c->device) {
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+  }
+  return MR_OK;
+}
+
+uint64_t block_elems(int type) { return type == MR_GGML_MXFP4 ? 32u : 256u; }
+
+bool valid_type(int type) { return type == MR_GGML_MXFP4 || type == MR_GGML_Q4_K; }
+
+constexpr uint64_t kAlign = 256;
+uint64_t align_up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+int pack_common(mr_ctx* c, int type, const void* bytes, uint64_t nbytes, uint32_t E, uint32_t out,
+                uint32_t in, const uint64_t* host_offsets, mr_pack** res) {
+  if (!res) return set_err(c, MR_E_INVAL, "out pointer is NULL");
+  *res = nullptr;
+  if (!valid_type(type)) return set_err(c, MR_E_UNSUPPORTED, "ggml type %d is not MXFP4 (39) or Q4_K (12)", type);
+  if (!bytes) return set_err(c, MR_E_INVAL, "weight bytes are NULL");
+  if (E == 0 || out == 0 || in == 0) return set_err(c, MR_E_INVAL, "empty expert shape E=%u out=%u in=%u", E, out, in);
+  if (in % block_elems(type) != 0)
+    return set_err(c, MR_E_INVAL, "in_features %u is not a multiple of the %llu-element block", in,
+                   (unsigned long long)block_elems(type));
+  const uint64_t mb = mr_matrix_bytes(type, out, in);
+  std::vector<uint64_t> off(E);
+  for (uint32_t e = 0; e < E; ++e) {
+    off[e] = host_offsets ? host_offsets[e] : (uint64_t)e * mb;
+    if (off[e] > nbytes || nbytes - off[e] < mb)
+      return set_err(c, MR_E_INVAL, "expert %u slice [%llu, +%llu) exceeds %llu bytes", e,
+                     (unsigned long long)off[e], (unsigned long long)mb, (unsigned long long)nbytes);
+    if (type == MR_GGML_Q4_K && (off[e] % 4 != 0))
+      return set_err(c, MR_E_INVAL, "Q4_K expert %u offset %llu is not 4-byte aligned", e,
+                     (unsigned long long)off[e]);
+  }
+  mr_pack* p = new (std::nothrow) mr_pack;
+  if (!p) return set_err(c, MR_E_NOMEM, "host allocation failed");
+  p->ctx = c;
+  p->type = type;
+  p->n_experts = E;
+  p->out_features = out;
+  p->in_features = in;
+  p->nbytes = nbytes;
+  p->matrix_bytes = mb;
+  p->h_offsets = std::move(off);
+  *res = p;
+  return MR_OK;
+}
+
+int upload_offsets(mr_ctx* c, mr_pack* p) {
+  if (!has_dev(c)) return MR_OK;
+  hipError_t e = hipMalloc(&p->d_offsets, sizeof(uint64_t) * p->n_experts);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(offsets)");
+  e = hipMemcpy(p->d_offsets, p->h_offsets.data(), sizeof(uint64_t) * p->n_experts,
+                hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMemcpy(offsets)");
+  return MR_OK;
+}
+
+// Scratch layout for T tokens of a layer shape.
+struct ScratchPlan {
+  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, total;
+};
+
+ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
+  ScratchPlan p{};
+  uint64_t o = 0;
+  p.idx = o, o += align_up(T * k * 4);
+  p.w = o, o += align_up(T * k * 4);
+  p.logits = o, o += align_up(T * E * 4);
+  p.act = o, o += align_up(T * k * I * 4);
+  p.act_sh = o, o += align_up(T * (Ish + 1) * 4);
+  // MFMA B-operand images: x split (H/32 blocks) and act split (k*I/32 blocks),
+  // 16 columns x 33 bytes per block, rounded generously.
+  p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40);
+  p.sync = o, o += align_up(4096 + E * 64);
+  p.groups = o, o += align_up((T * k + E + 64) * 8);
+  p.total = o;
+  return p;
+}
+
+int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
+  mr::Scratch& s = c->scratch;
+  uint64_t k = L->d.top_k, E = L->E, I = L->I, H = L->H, Ish = L->Ish;
+  if (s.base && T <= s.cap_tokens && k <= s.cap_k && E <= s.cap_e && I <= s.cap_i && H <= s.cap_h &&
+      Ish <= s.cap_ish)
+    return MR_OK;
+  if (c->capturing)
+    return set_err(c, MR_E_INVAL, "scratch too small during graph capture; call mr_reserve first");
+  uint64_t nT = std::max<uint64_t>(T, s.cap_tokens), nk = std::max<uint64_t>(k, s.cap_k);
+  uint64_t nE = std::max<uint64_t>(E, s.cap_e), nI = std::max<uint64_t>(I, s.cap_i);
+  uint64_t nH = std::max<uint64_t>(H, s.cap_h), nS = std::max<uint64_t>(Ish, s.cap_ish);
+  ScratchPlan p = plan_scratch(nT, nk, nE, nI, nH, nS);
+  if (s.base) {
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+    (void)hipFree(s.base);
+    s.base = nullptr;
+  }
+  void* base = nullptr;
+  hipError_t e = hipMalloc(&base, p.total);
+  if (e != hipSuccess) {
+    s = mr::Scratch{};
+    return hip_fail(c, e, "hipMalloc(scratch)");
+  }
+  // sync words and counters must start at zero; later calls keep them balanced
+  e = mr::launch_zero(mr::Launch{c->stream, nullptr}, base, p.total);
+  if (e != hipSuccess) return hip_fail(c, e, "zero scratch");
+  char* b = static_cast<char*>(base);
+  s.base = base;
+  s.bytes = p.total;
+  s.idx = reinterpret_cast<int32_t*>(b + p.idx);
+  s.w = reinterpret_cast<float*>(b + p.w);
+  s.logits = reinterpret_cast<float*>(b + p.logits);
+  s.act = reinterpret_cast<float*>(b + p.act);
+  s.act_sh = reinterpret_cast<float*>(b + p.act_sh);
+  s.mfma_b = b + p.mfma_b;
+  s.sync = reinterpret_cast<uint32_t*>(b + p.sync);
+  s.groups = reinterpret_cast<int32_t*>(b + p.groups);
+  s.cap_tokens = nT, s.cap_k = nk, s.cap_e = nE, s.cap_i = nI, s.cap_h = nH, s.cap_ish = nS;
+  return MR_OK;
+}
+
+int check_layer(mr_ctx* c, const mr_layer* L) {
+  if (!L) return set_err(c, MR_E_INVAL, "layer is NULL");
+  if (L->ctx != c) return set_err(c, MR_E_INVAL, "layer belongs to another context");
+  return MR_OK;
+}
+
+}  // namespace
+
+namespace mr {
+
+hipEvent_t Prof::next_event() {
+  if (used == pool.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    pool.push_back(e);
+  }
+  return pool[used++];
+}
+
+int Prof::name_id(const char* n) {
+  for (size_t i = 0; i < names.size(); ++i)
+    if (names[i] == n) return (int)i;
+  names.emplace_back(n);
+  return (int)names.size() - 1;
+}
+
+}  // namespace mr
+
+extern "C" {
+
+const char* mr_status_string(int status) {
+  switch (status) {
+    case MR_OK: return "ok";
+    case MR_E_INVAL: return "invalid argument";
+    case MR_E_NOMEM: return "out of device memory";
+    case MR_E_NODEV: return "no HIP device";
+    case MR_E_LAUNCH: return "HIP launch or runtime failure";
+    case MR_E_UNSUPPORTED: return "unsupported";
+    default: return "unknown status";
+  }
+}
+
+const char* mr_last_error(const mr_ctx* ctx) { return ctx ? ctx->err.c_str() : g_err.c_str(); }
+
+int mr_ctx_create(int device, mr_ctx** out) {
+  if (!out) return set_err(nullptr, MR_E_INVAL, "out pointer is NULL");
+  *out = nullptr;
+  if (device < MR_DEVICE_NONE) return set_err(nullptr, MR_E_INVAL, "device %d is invalid", device);
+  mr_ctx* c = new (std::nothrow) mr_ctx;
+  if (!c) return set_err(nullptr, MR_E_NOMEM, "host allocation failed");
+  if (device == MR_DEVICE_NONE) {
+    *out = c;
+    return MR_OK;
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    delete c;
+    return set_err(nullptr, MR_E_NODEV, "no HIP device visible");
+  }
+  if (device >= n) {
+    delete c;
+    return set_err(nullptr, MR_E_INVAL, "device %d out of range (have %d)", device, n);
+  }
+  hipError_t e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&c->ev0);
+  if (e == hipSuccess) e = hipEventCreate(&c->ev1);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) {
+    int rc = hip_fail(nullptr, e, "context setup");
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return rc;
+  }
+  c->device = device;
+  c->own_stream = true;
+  *out = c;
+  return MR_OK;
+}
+
+void mr_ctx_destroy(mr_ctx* c) {
+  if (!c) return;
+  if (has_dev(c)) {
+    (void)bind(c);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->scratch.base) (void)hipFree(c->scratch.base);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    for (hipEvent_t ev : c->prof.pool) (void)hipEventDestroy(ev);
+    if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
+  }
+  delete c;
+}
+
+int mr_ctx_device(const mr_ctx* c) { return c ? c->device : MR_DEVICE_NONE; }
+
+int mr_ctx_set_stream(mr_ctx* c, void* hip_stream) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context has no stream");
+  if (c->capturing) return set_err(c, MR_E_INVAL, "cannot change stream during capture");
+  if (c->own_stream && c->stream) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipStreamDestroy(c->stream);
+  }
+  c->stream = static_cast<hipStream_t>(hip_stream);
+  c->own_stream = false;
+  return MR_OK;
+}
+
+void* mr_ctx_stream(const mr_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int mr_ctx_set_option(mr_ctx* c, int option, int value) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (option == MR_OPT_DECODE_KERNEL) {
+    if (value < MR_DECODE_AUTO || value > MR_DECODE_MFMA)
+      return set_err(c, MR_E_INVAL, "decode kernel %d unknown", value);
+    c->decode_kernel = value;
+    return MR_OK;
+  }
+  if (option == MR_OPT_PROFILE) {
+    if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+    c->prof.on = value != 0;
+    return MR_OK;
+  }
+  return set_err(c, MR_E_INVAL, "option %d unknown", option);
+}
+
+int mr_sync(mr_ctx* c) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipStreamSynchronize(c->stream);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipStreamSynchronize");
+}
+
+int mr_dev_alloc(mr_ctx* c, uint64_t nbytes, void** out) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!out) return set_err(c, MR_E_INVAL, "out pointer is NULL");
+  *out = nullptr;
+  if (nbytes == 0) return set_err(c, MR_E_INVAL, "zero-byte allocation");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if (c->capturing) return set_err(c, MR_E_INVAL, "allocation during graph capture");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipMalloc(out, nbytes);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipMalloc");
+}
+
+int mr_dev_free(mr_ctx* c, void* p) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!p) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  (void)hipStreamSynchronize(c->stream);
+  hipError_t e = hipFree(p);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipFree");
+}
+
+int mr_upload(mr_ctx* c, void* dst, const void* src, uint64_t n) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if ((!dst || !src) && n) return set_err(c, MR_E_INVAL, "NULL buffer");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if (n == 0) return MR_OK;
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "upload");
+}
+
+int mr_download(mr_ctx* c, void* dst, const void* src, uint64_t n) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if ((!dst || !src) && n) return set_err(c, MR_E_INVAL, "NULL buffer");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if (n == 0) return MR_OK;
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "download");
+}
+
+int mr_dev_zero(mr_ctx* c, void* dst, uint64_t n) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!dst && n) return set_err(c, MR_E_INVAL, "NULL buffer");
+  if (n % 4) return set_err(c, MR_E_INVAL, "zero fill size %llu is not a multiple of 4", (unsigned long long)n);
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = mr::launch_zero(c->launch(), dst, n);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "zero fill");
+}
+
+uint64_t mr_matrix_bytes(int type, uint64_t rows, uint64_t cols) {
+  if (type == MR_GGML_MXFP4) return rows * (cols / 32) * 17;
+  if (type == MR_GGML_Q4_K) return rows * (cols / 256) * 144;
+  return 0;
+}
+
+int mr_pack_upload(mr_ctx* c, int type, const void* host_bytes, uint64_t nbytes, uint32_t E,
+                   uint32_t out, uint32_t in, const uint64_t* host_offsets, mr_pack** res) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = pack_common(c, type, host_bytes, nbytes, E, out, in, host_offsets, res);
+  if (rc) return rc;
+  mr_pack* p = *res;
+  if (!has_dev(c)) {
+    // host-only: keep the layout, no device copy (used by validation tests)
+    p->base = static_cast<const uint8_t*>(host_bytes);
+    return MR_OK;
+  }
+  if ((rc = bind(c))) {
+    delete p, *res = nullptr;
+    return rc;
+  }
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, nbytes + 64);
+  if (e != hipSuccess) {
+    delete p, *res = nullptr;
+    return hip_fail(c, e, "hipMalloc(pack)");
+  }
+  e = hipMemcpy(d, host_bytes, nbytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    delete p, *res = nullptr;
+    return hip_fail(c, e, "hipMemcpy(pack)");
+  }
+  p->base = static_cast<const uint8_t*>(d);
+  p->owned = true;
+  if ((rc = upload_offsets(c, p))) {
+    mr_pack_destroy(p), *res = nullptr;
+    return rc;
+  }
+  return MR_OK;
+}
+
+int mr_pack_wrap(mr_ctx* c, int type, const void* dev_bytes, uint64_t nbytes, uint32_t E,
+                 uint32_t out, uint32_t in, const uint64_t* host_offsets, mr_pack** res) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = pack_common(c, type, dev_bytes, nbytes, E, out, in, host_offsets, res);
+  if (rc) return rc;
+  mr_pack* p = *res;
+  if (type == MR_GGML_Q4_K && (reinterpret_cast<uintptr_t>(dev_bytes) % 4 != 0)) {
+    delete p, *res = nullptr;
+    return set_err(c, MR_E_INVAL, "Q4_K device bytes must be 4-byte aligned");
+  }
+  p->base = static_cast<const uint8_t*>(dev_bytes);
+  if (has_dev(c)) {
+    if ((rc = bind(c)) || (rc = upload_offsets(c, p))) {
+      mr_pack_destroy(p), *res = nullptr;
+      return rc;
+    }
+  }
+  return MR_OK;
+}
+
+void mr_pack_destroy(mr_pack* p) {
+  if (!p) return;
+  if (has_dev(p->ctx)) {
+    (void)bind(p->ctx);
+    (void)hipStreamSynchronize(p->ctx->stream);
+    if (p->owned && p->base) (void)hipFree(const_cast<uint8_t*>(p->base));
+    if (p->d_offsets) (void)hipFree(p->d_offsets);
+  }
+  delete p;
+}
+
+int mr_dequant(mr_ctx* c, const mr_pack* p, uint32_t expert, float* out) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!p || !out) return set_err(c, MR_E_INVAL, "NULL pack or output");
+  if (p->ctx != c) return set_err(c, MR_E_INVAL, "pack belongs to another context");
+  if (expert >= p->n_experts) return set_err(c, MR_E_INVAL, "expert %u out of range (E=%u)", expert, p->n_experts);
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = mr::launch_dequant(c->launch(), *p, expert, out);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "dequant launch");
+}
+
+int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!d || !res) return set_err(c, MR_E_INVAL, "NULL descriptor or out pointer");
+  *res = nullptr;
+  if (!d->gate || !d->up || !d->down) return set_err(c, MR_E_INVAL, "gate, up and down packs are required");
+  if (d->gate->ctx != c || d->up->ctx != c || d->down->ctx != c)
+    return set_err(c, MR_E_INVAL, "packs belong to another context");
+  const int type = d->gate->type;
+  if (d->up->type != type || d->down->type != type)
+    return set_err(c, MR_E_INVAL, "gate/up/down packs have different block types");
+  const uint32_t E = d->gate->n_experts, I = d->gate->out_features, H = d->gate->in_features;
+  if (d->up->n_experts != E || d->down->n_experts != E)
+    return set_err(c, MR_E_INVAL, "expert counts differ (%u/%u/%u)", E, d->up->n_experts, d->down->n_experts);
+  if (d->up->out_features != I || d->up->in_features != H)
+    return set_err(c, MR_E_INVAL, "up pack is [%u,%u], expected [%u,%u]", d->up->out_features, d->up->in_features, I, H);
+  if (d->down->out_features != H || d->down->in_features != I)
+    return set_err(c, MR_E_INVAL, "down pack is [%u,%u], expected [%u,%u]", d->down->out_features, d->down->in_features, H, I);
+  if (!d->router_w) return set_err(c, MR_E_INVAL, "router weights are required");
+  if (E > mr::kMaxExperts) return set_err(c, MR_E_UNSUPPORTED, "n_experts %u > %u", E, mr::kMaxExperts);
+  if (d->top_k == 0 || d->top_k > mr::kMaxTopK || d->top_k > E)
+    return set_err(c, MR_E_INVAL, "top_k %u must be in 1..min(16, E=%u)", d->top_k, E);
+  if (d->act != MR_ACT_SILU && d->act != MR_ACT_SWIGLU_OAI) return set_err(c, MR_E_INVAL, "activation %u unknown", d->act);
+  if (d->route_flags & ~(MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK))
+    return set_err(c, MR_E_INVAL, "unknown routing flags 0x%x", d->route_flags);
+  if (H > mr::kMaxHidden) return set_err(c, MR_E_UNSUPPORTED, "hidden %u > %u", H, mr::kMaxHidden);
+  uint32_t Ish = 0;
+  const bool any_sh = d->sh_gate || d->sh_up || d->sh_down;
+  if (any_sh) {
+    if (!d->sh_gate || !d->sh_up || !d->sh_down)
+      return set_err(c, MR_E_INVAL, "shared expert needs gate, up and down packs");
+    if (d->sh_gate->ctx != c || d->sh_up->ctx != c || d->sh_down->ctx != c)
+      return set_err(c, MR_E_INVAL, "shared packs belong to another context");
+    if (d->sh_gate->type != d->sh_up->type)
+      return set_err(c, MR_E_INVAL, "shared gate/up packs have different block types");
+    Ish = d->sh_gate->out_features;
+    if (d->sh_gate->n_experts != 1 || d->sh_up->n_experts != 1 || d->sh_down->n_experts != 1)
+      return set_err(c, MR_E_INVAL, "shared expert packs must hold exactly one expert");
+    if (d->sh_gate->in_features != H || d->sh_up->out_features != Ish || d->sh_up->in_features != H ||
+        d->sh_down->out_features != H || d->sh_down->in_features != Ish)
+      return set_err(c, MR_E_INVAL, "shared expert shapes do not match hidden %u / inter %u", H, Ish);
+  }
+  if ((uint64_t)d->top_k * I + Ish > mr::kMaxHidden)
+    return set_err(c, MR_E_UNSUPPORTED, "top_k*inter + shared inter = %llu exceeds %u",
+                   (unsigned long long)d->top_k * I + Ish, mr::kMaxHidden);
+  mr_layer* L = new (std::nothrow) mr_layer;
+  if (!L) return set_err(c, MR_E_NOMEM, "host allocation failed");
+  L->ctx = c;
+  L->d = *d;
+  L->H = H, L->I = I, L->E = E, L->Ish = Ish, L->type = type;
+  *res = L;
+  return MR_OK;
+}
+
+void mr_layer_destroy(mr_layer* L) { delete L; }
+
+int mr_reserve(mr_ctx* c, const mr_layer* L, uint32_t max_tokens) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (max_tokens == 0) return set_err(c, MR_E_INVAL, "max_tokens is 0");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c))) return rc;
+  return ensure_scratch(c, L, max_tokens);
+}
+
+int mr_router_topk(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, int32_t* idx,
+                   float* w, float* logits) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !idx || !w) return set_err(c, MR_E_INVAL, "NULL x, idx or w");
+  if (T == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
+  float* lg = logits ? logits : c->scratch.logits;
+  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, T, lg);
+  if (e == hipSuccess) e = mr::launch_topk(c->launch(), lg, T, L->E, L->d.top_k, L->d.route_flags, idx, w);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "router launch");
+}
+
+int mr_topk(mr_ctx* c, const float* logits, uint32_t T, uint32_t E, uint32_t k, uint32_t flags,
+            int32_t* idx, float* w) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!logits || !idx || !w) return set_err(c, MR_E_INVAL, "NULL logits, idx or w");
+  if (E == 0 || E > mr::kMaxExperts) return set_err(c, MR_E_INVAL, "n_experts %u must be in 1..%u", E, mr::kMaxExperts);
+  if (k == 0 || k > mr::kMaxTopK || k > E) return set_err(c, MR_E_INVAL, "top_k %u must be in 1..min(16, %u)", k, E);
+  if (flags & ~(MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK)) return set_err(c, MR_E_INVAL, "unknown routing flags 0x%x", flags);
+  if (T == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = mr::launch_topk(c->launch(), logits, T, E, k, flags, idx, w);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "topk launch");
+}
+
+int mr_moe_experts(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, const int32_t* idx,
+                   const float* w, float* y) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !idx || !w || !y) return set_err(c, MR_E_INVAL, "NULL x, idx, w or y");
+  if (T == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
+  hipError_t e = mr::launch_experts_valu(c->launch(), *L, x, T, idx, w, c->scratch.act,
+                                         c->scratch.act_sh, y);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "expert launch");
+}
+
+int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c)) || (rc = ensure_scratch(c, L, 1))) return rc;
+  mr::Scratch& s = c->scratch;
+  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, 1, s.logits);
+  if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
+  if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, 1, s.idx, s.w, s.act, s.act_sh, y);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "moe forward launch");
+}
+
+int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if (T == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
+  mr::Scratch& s = c->scratch;
+  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, T, s.logits);
+  if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, T, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
+  if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch");
+}
+
+int mr_graph_begin(mr_ctx* c) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if (c->capturing) return set_err(c, MR_E_INVAL, "capture already in progress");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamBeginCapture");
+  c->capturing = true;
+  return MR_OK;
+}
+
+int mr_graph_end(mr_ctx* c, mr_graph** out) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!out) return set_err(c, MR_E_INVAL, "out pointer is NULL");
+  *out = nullptr;
+  if (!c->capturing) return set_err(c, MR_E_INVAL, "no capture in progress");
+  c->capturing = false;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
+  mr_graph* G = new (std::nothrow) mr_graph;
+  if (!G) {
+    (void)hipGraphDestroy(g);
+    return set_err(c, MR_E_NOMEM, "host allocation failed");
+  }
+  G->graph = g;
+  e = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    mr_graph_destroy(G);
+    return hip_fail(c, e, "hipGraphInstantiate");
+  }
+  *out = G;
+  return MR_OK;
+}
+
+int mr_graph_launch(mr_ctx* c, const mr_graph* G) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!G || !G->exec) return set_err(c, MR_E_INVAL, "graph is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipGraphLaunch(G->exec, c->stream);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipGraphLaunch");
+}
+
+void mr_graph_destroy(mr_graph* G) {
+  if (!G) return;
+  if (G->exec) (void)hipGraphExecDestroy(G->exec);
+  if (G->graph) (void)hipGraphDestroy(G->graph);
+  delete G;
+}
+
+int mr_timer_start(mr_ctx* c) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipEventRecord(c->ev0, c->stream);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipEventRecord");
+}
+
+int mr_timer_stop(mr_ctx* c, float* ms) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!ms) return set_err(c, MR_E_INVAL, "out pointer is NULL");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipEventRecord(c->ev1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(c->ev1);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, c->ev0, c->ev1);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "timer");
+}
+
+int mr_profile_read(mr_ctx* c, const char* kernel, uint64_t* count, double* total_ms) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!kernel || !count || !total_ms) return set_err(c, MR_E_INVAL, "NULL argument");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  uint64_t n = 0;
+  double tot = 0.0;
+  for (const auto& r : c->prof.recs) {
+    if (c->prof.names[r.name] != kernel) continue;
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventElapsedTime");
+    ++n, tot += ms;
+  }
+  *count = n, *total_ms = tot;
+  return MR_OK;
+}
+
+int mr_profile_reset(mr_ctx* c) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (has_dev(c)) {
+    int rc = bind(c);
+    if (rc) return rc;
+    (void)hipStreamSynchronize(c->stream);
+  }
+  c->prof.recs.clear();
+  c->prof.used = 0;
+  return MR_OK;
+}
+
+int mr_synth_blocks(mr_ctx* c, int type, void* dst, uint64_t n_blocks, uint64_t seed) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!valid_type(type)) return set_err(c, MR_E_UNSUPPORTED, "ggml type %d", type);
+  if (!dst && n_blocks) return set_err(c, MR_E_INVAL, "NULL destination");
+  if (n_blocks == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  hipError_t e = mr::launch_synth(c->launch(), type, dst, n_blocks, seed);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "synth launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,132 @@
+// mr_internal.h -- host-side objects behind the C ABI of include/moe_rocm.h,
+// shared by the API layer (mr_api.cpp) and the kernel launchers (*.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/moe_rocm.h"
+
+namespace mr {
+
+constexpr uint32_t kMaxTopK = 16;        // softmax_topk_kernel limit (fused_ops.metal:150)
+constexpr uint32_t kMaxExperts = 512;    // same limit (fused_ops.metal:158)
+constexpr uint32_t kMaxHidden = 16384;   // LDS-staged activation limit of the VALU kernels
+
+// Per-context scratch: routing outputs, intermediate activations, sync words.
+// Sized by mr_reserve (or lazily on first use outside graph capture).
+struct Scratch {
+  void* base = nullptr;
+  uint64_t bytes = 0;
+  // carve-outs (device pointers into base)
+  int32_t* idx = nullptr;      // [T, k]
+  float* w = nullptr;          // [T, k]
+  float* logits = nullptr;     // [T, E]
+  float* act = nullptr;        // [T, k, I] or grouped [T*k, I]
+  float* act_sh = nullptr;     // [T, Ish] shared expert activation
+  void* mfma_b = nullptr;      // MFMA B-operand images (x split / act split)
+  uint32_t* sync = nullptr;    // sync words for the fused decode kernel
+  int32_t* groups = nullptr;   // batched path: per-expert token lists
+  uint64_t cap_tokens = 0, cap_k = 0, cap_e = 0, cap_i = 0, cap_h = 0, cap_ish = 0;
+};
+
+// Optional per-kernel timing: an event pair around every kernel launch on the
+// context stream (enabled by MR_OPT_PROFILE, never during graph capture).
+struct Prof {
+  bool on = false;
+  struct Rec {
+    int name;
+    hipEvent_t a, b;
+  };
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
+  std::vector<Rec> recs;
+  std::vector<std::string> names;
+  hipEvent_t next_event();
+  int name_id(const char* n);
+};
+
+// What a launcher needs: the stream and, when profiling, the recorder.
+struct Launch {
+  hipStream_t s;
+  Prof* prof;  // nullptr when not profiling
+};
+
+// RAII bracket around one kernel launch.
+struct ProfScope {
+  Launch L;
+  const char* name;
+  hipEvent_t a = nullptr;
+  ProfScope(const Launch& l, const char* n) : L(l), name(n) {
+    if (L.prof) {
+      a = L.prof->next_event();
+      (void)hipEventRecord(a, L.s);
+    }
+  }
+  ~ProfScope() {
+    if (L.prof && a) {
+      hipEvent_t b = L.prof->next_event();
+      (void)hipEventRecord(b, L.s);
+      L.prof->recs.push_back({L.prof->name_id(name), a, b});
+    }
+  }
+};
+
+}  // namespace mr
+
+struct mr_ctx {
+  int device = MR_DEVICE_NONE;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  int n_cu = 0;
+  int decode_kernel = MR_DECODE_AUTO;
+  std::string err;
+  mr::Scratch scratch;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  bool capturing = false;
+  mr::Prof prof;
+  mr::Launch launch() { return mr::Launch{stream, (prof.on && !capturing) ? &prof : nullptr}; }
+};
+
+struct mr_pack {
+  mr_ctx* ctx = nullptr;
+  int type = 0;
+  uint32_t n_experts = 0, out_features = 0, in_features = 0;
+  const uint8_t* base = nullptr;   // device bytes
+  uint64_t nbytes = 0;
+  bool owned = false;
+  uint64_t matrix_bytes = 0;       // bytes of one expert matrix
+  std::vector<uint64_t> h_offsets; // per-expert byte offsets from base
+  uint64_t* d_offsets = nullptr;   // same on the device (nullptr for host-only ctx)
+};
+
+struct mr_layer {
+  mr_ctx* ctx = nullptr;
+  mr_layer_desc d{};
+  uint32_t H = 0, I = 0, E = 0, Ish = 0;
+  int type = 0;
+};
+
+struct mr_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace mr {
+
+// Launchers implemented in the .hip files. Each returns a hipError_t from the launch.
+hipError_t launch_zero(const Launch& L, void* dst, uint64_t nbytes);
+hipError_t launch_router_logits(const Launch& K, const mr_layer& L, const float* x, uint32_t T,
+                                float* logits);
+hipError_t launch_topk(const Launch& K, const float* logits, uint32_t T, uint32_t E, uint32_t k,
+                       uint32_t flags, int32_t* idx, float* w);
+hipError_t launch_experts_valu(const Launch& K, const mr_layer& L, const float* x, uint32_t T,
+                               const int32_t* idx, const float* w, float* act, float* act_sh,
+                               float* y);
+hipError_t launch_dequant(const Launch& K, const mr_pack& p, uint32_t expert, float* out);
+hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+
+}  // namespace mr

@@ -1,0 +1,233 @@
+"""GPU (HIP, gfx950) vs CPU oracle parity, through the C ABI.
+
+Bars (north star): dequantized weights and top-k indices bit-exact; layer
+outputs within max relative error 1e-3, measured as
+max_i |y_gpu - y_ref| / max_i |y_ref| (fp32 accumulation on both sides).
+"""
+import numpy as np
+import pytest
+
+import moe_rocm as M
+import npref
+import oracle
+from moe_rocm import synth as S
+from moe_rocm import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+# ---- generator and dequant ------------------------------------------------------
+
+@pytest.mark.parametrize("ggml_type,n", [(M.GGML_MXFP4, 300_001), (M.GGML_Q4_K, 40_003)])
+def test_synth_gpu_equals_host(gpu_ctx, ggml_type, n):
+    seed = S.stream_seed(77, 1, 2, 3)
+    buf = gpu_ctx.alloc(n * S.block_bytes(ggml_type))
+    gpu_ctx.synth_blocks(ggml_type, buf, n, seed)
+    got = buf.download(np.uint8, n * S.block_bytes(ggml_type))
+    assert np.array_equal(got, S.blocks(ggml_type, seed, n))
+    buf.free()
+
+
+def test_dequant_mxfp4_bit_exact_all_codes(gpu_ctx):
+    blocks = np.zeros((256, 17), dtype=np.uint8)
+    blocks[:, 0] = np.arange(256)
+    j = np.arange(16)
+    blocks[:, 1:] = (j | ((15 - j) << 4)).astype(np.uint8)
+    # a "matrix" of 256 rows x 32 columns, one block per row: every code x every exponent
+    pack = M.ExpertPack.upload(gpu_ctx, M.GGML_MXFP4, blocks.reshape(-1), 1, 256, 32)
+    got = pack.dequant(0).reshape(-1)
+    want = oracle.dequant_mxfp4(blocks.reshape(-1), 256 * 32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    pack.close()
+
+
+@pytest.mark.parametrize("ggml_type,out_f,in_f,E", [(M.GGML_MXFP4, 2880, 2880, 3),
+                                                    (M.GGML_MXFP4, 90, 2880, 5),
+                                                    (M.GGML_Q4_K, 768, 2048, 3),
+                                                    (M.GGML_Q4_K, 2048, 512, 2)])
+def test_dequant_bit_exact_random(gpu_ctx, ggml_type, out_f, in_f, E):
+    per = out_f * in_f // S.block_elems(ggml_type)
+    data = S.blocks(ggml_type, S.stream_seed(78, ggml_type, out_f, in_f), E * per)
+    pack = M.ExpertPack.upload(gpu_ctx, ggml_type, data, E, out_f, in_f)
+    mb = S.matrix_bytes(ggml_type, out_f, in_f)
+    for e in range(E):
+        got = pack.dequant(e).reshape(-1)
+        want = oracle.dequant(ggml_type, data[e * mb:(e + 1) * mb], out_f * in_f)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), e
+    pack.close()
+
+
+# ---- routing -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("E,k", [(32, 4), (128, 8), (384, 10), (512, 16), (7, 7)])
+@pytest.mark.parametrize("flags", [M.ROUTE_SOFTMAX_AFTER_TOPK, M.ROUTE_NORM_TOPK, 0])
+def test_topk_exact_on_given_logits(gpu_ctx, E, k, flags):
+    rng = np.random.default_rng(E + 1000 * k + flags)
+    T = 33
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[1, 3] = logits[1, E - 1] = logits[1].max() + 0.5   # exact tie -> lower index
+    logits[2, : E // 2] = -np.inf                             # masked (dummy) experts
+    logits[3, :] = 0.25                                       # all equal
+    d_l = gpu_ctx.to_device(logits)
+    d_i = gpu_ctx.alloc(T * k * 4)
+    d_w = gpu_ctx.alloc(T * k * 4)
+    M.topk(gpu_ctx, d_l, T, E, k, flags, d_i, d_w)
+    gi = d_i.download(np.int32).reshape(T, k)
+    gw = d_w.download(np.float32).reshape(T, k)
+    ri, rw = oracle.topk_routing(logits, k, bool(flags & 2), bool(flags & 1))
+    assert np.array_equal(gi, ri.astype(np.int32))
+    assert np.allclose(gw, rw, rtol=1e-5, atol=1e-7)
+
+
+# ---- layers --------------------------------------------------------------------------
+
+TINY_MX = W.LayerSpec(201, 0, W.GGML_MXFP4, 512, 384, 8, 2, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                      W.ACT_SWIGLU_OAI, True, True)
+TINY_Q4 = W.LayerSpec(202, 0, W.GGML_Q4_K, 1024, 512, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                      False, False)
+TINY_SH = W.LayerSpec(203, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                      False, False, sh_inter=256)
+SPECS = {
+    "tiny-mxfp4": TINY_MX,
+    "tiny-q4k": TINY_Q4,
+    "tiny-q4k-shared": TINY_SH,
+    "C1-gpt-oss": W.gpt_oss(1, 0),
+    "C3-qwen3-layer0": W.qwen3_30b(3, 0),
+    "C4-coder-next-layer0": W.coder_next(4, 0),
+}
+
+
+@pytest.fixture(scope="module")
+def layers(gpu_ctx):
+    built = {}
+    yield built
+    for dl, _ in built.values():
+        dl.close()
+
+
+def get_layer(gpu_ctx, layers, name):
+    if name not in layers:
+        spec = SPECS[name]
+        dl = W.DeviceLayer(gpu_ctx, spec)
+        host = dict(spec=spec)
+        host.update(dl.download_quant())
+        host.update(W.float_tensors(spec))
+        layers[name] = (dl, host)
+    return layers[name]
+
+
+@pytest.mark.parametrize("name", list(SPECS))
+def test_forward_decode_parity(gpu_ctx, layers, name):
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    L = oracle.layer_from_host(host)
+    x = W.x_tokens(spec, 2)
+    for t in range(2):
+        dx = gpu_ctx.to_device(x[t])
+        dy = gpu_ctx.alloc(spec.hidden * 4)
+        dl.layer.forward(dx, dy)
+        y = dy.download(np.float32)
+        ry, ridx, rw, rlg = L.forward(x[t])
+        # routing: GPU logits drive the same top-k unless the k-th/(k+1)-th gap is a rounding tie
+        s = np.sort(rlg[0])[::-1]
+        gap = s[spec.top_k - 1] - s[spec.top_k]
+        if gap > 1e-5 * np.abs(rlg).max():
+            assert rel_err(y, ry[0]) <= REL_TOL, (name, t, rel_err(y, ry[0]))
+        dx.free(), dy.free()
+
+
+@pytest.mark.parametrize("name", list(SPECS))
+def test_router_topk_parity(gpu_ctx, layers, name):
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    L = oracle.layer_from_host(host)
+    T = 8
+    x = W.x_tokens(spec, T, first_token=10)
+    dx = gpu_ctx.to_device(x)
+    di, dw, dlg = gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.n_experts * 4)
+    dl.layer.router_topk(dx, T, di, dw, dlg)
+    gi = di.download(np.int32).reshape(T, -1)
+    gw = dw.download(np.float32).reshape(T, -1)
+    glg = dlg.download(np.float32).reshape(T, -1)
+    _, ridx, rw, rlg = L.forward(x)
+    assert np.allclose(glg, rlg, rtol=1e-4, atol=1e-5 * np.abs(rlg).max())
+    for t in range(T):
+        s = np.sort(rlg[t])[::-1]
+        if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg[t]).max():
+            assert np.array_equal(gi[t], ridx[t].astype(np.int32)), t
+            assert np.allclose(gw[t], rw[t], rtol=1e-4, atol=1e-6)
+    for b in (dx, di, dw, dlg):
+        b.free()
+
+
+@pytest.mark.parametrize("name", ["tiny-mxfp4", "tiny-q4k", "tiny-q4k-shared", "C1-gpt-oss"])
+def test_experts_given_routing_parity(gpu_ctx, layers, name):
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    L = oracle.layer_from_host(host)
+    T = 3
+    x = W.x_tokens(spec, T, first_token=20)
+    rng = np.random.default_rng(5)
+    idx = np.stack([rng.choice(spec.n_experts, spec.top_k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.05, 1.0, (T, spec.top_k)).astype(np.float32)
+    dx, di, dw = gpu_ctx.to_device(x), gpu_ctx.to_device(idx), gpu_ctx.to_device(w)
+    dy = gpu_ctx.alloc(T * spec.hidden * 4)
+    dl.layer.experts(dx, T, di, dw, dy)
+    y = dy.download(np.float32).reshape(T, -1)
+    ry = L.experts(x, idx.astype(np.uint32), w)
+    for t in range(T):
+        assert rel_err(y[t], ry[t]) <= REL_TOL, (t, rel_err(y[t], ry[t]))
+    if name.startswith("tiny"):
+        fy, _, _, _ = npref.moe_forward(host, x, idx=idx, w=w)
+        for t in range(T):
+            assert rel_err(y[t], fy[t]) <= REL_TOL
+    for b in (dx, di, dw, dy):
+        b.free()
+
+
+@pytest.mark.parametrize("name,T", [("tiny-mxfp4", 37), ("tiny-q4k-shared", 16), ("C1-gpt-oss", 64)])
+def test_batched_parity(gpu_ctx, layers, name, T):
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    L = oracle.layer_from_host(host)
+    x = W.x_tokens(spec, T, first_token=100)
+    dx = gpu_ctx.to_device(x)
+    dy = gpu_ctx.alloc(T * spec.hidden * 4)
+    dl.layer.forward_batched(dx, T, dy)
+    y = dy.download(np.float32).reshape(T, -1)
+    ry, _, _, rlg = L.forward(x, n_threads=8)
+    for t in range(T):
+        s = np.sort(rlg[t])[::-1]
+        if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg[t]).max():
+            assert rel_err(y[t], ry[t]) <= REL_TOL, (t, rel_err(y[t], ry[t]))
+    dx.free(), dy.free()
+
+
+def test_graph_replay_matches_eager(gpu_ctx, layers):
+    dl, _ = get_layer(gpu_ctx, layers, "tiny-q4k-shared")
+    spec = dl.spec
+    dl.layer.reserve(4)
+    x = W.x_tokens(spec, 1, first_token=300)
+    dx = gpu_ctx.to_device(x[0])
+    dy_e, dy_g = gpu_ctx.alloc(spec.hidden * 4), gpu_ctx.alloc(spec.hidden * 4)
+    dl.layer.forward(dx, dy_e)
+    eager = dy_e.download(np.float32)
+    gpu_ctx.graph_begin()
+    dl.layer.forward(dx, dy_g)
+    g = gpu_ctx.graph_end()
+    for rep in range(4):
+        gpu_ctx.check(M.lib.mr_dev_zero(gpu_ctx.h, dy_g.ptr, spec.hidden * 4))
+        g.launch()
+        dl.layer.forward(dx, dy_e)  # eager work between replays
+        gpu_ctx.sync()
+        assert np.array_equal(dy_g.download(np.float32), eager), rep
+    g.close()
+    for b in (dx, dy_e, dy_g):
+        b.free()
