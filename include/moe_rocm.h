@@ -69,6 +69,10 @@ extern "C" {
 #define MR_DECODE_MFMA 2   /* scaled MX-fp4 MFMA matvec, single fused launch per layer */
 /* 1: record a HIP event pair around every kernel launch (read with mr_profile_read). */
 #define MR_OPT_PROFILE 2
+/* Iteration limit of the fused decode kernel's cross-workgroup waits (default
+ * 2^22, about 0.1 s). A wait that runs out ends the launch early and makes the
+ * next mr_sync return MR_E_LAUNCH; a value of 0 restores the default. */
+#define MR_OPT_SPIN_LIMIT 3
 
 typedef struct mr_ctx mr_ctx;
 typedef struct mr_pack mr_pack;
@@ -87,7 +91,8 @@ int mr_ctx_set_stream(mr_ctx* ctx, void* hip_stream);
 void* mr_ctx_stream(const mr_ctx* ctx);
 int mr_ctx_set_option(mr_ctx* ctx, int option, int value);
 /* Wait for all work enqueued on the context stream (the reference syncs at
- * to_vec1 readbacks, layer.rs:938, engine.rs:2069). */
+ * to_vec1 readbacks, layer.rs:938, engine.rs:2069). Also reports a fused decode
+ * launch that ended early (MR_E_LAUNCH) since the previous mr_sync. */
 int mr_sync(mr_ctx* ctx);
 
 /* ---- device memory ------------------------------------------------------- */

@@ -281,6 +281,11 @@ int mr_ctx_set_option(mr_ctx* c, int option, int value) {
     c->decode_kernel = value;
     return MR_OK;
   }
+  if (option == MR_OPT_SPIN_LIMIT) {
+    if (value < 0) return set_err(c, MR_E_INVAL, "spin limit %d is negative", value);
+    c->spin_limit = value == 0 ? (1u << 22) : (uint32_t)value;
+    return MR_OK;
+  }
   if (option == MR_OPT_PROFILE) {
     if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
     c->prof.on = value != 0;
@@ -295,7 +300,20 @@ int mr_sync(mr_ctx* c) {
   int rc = bind(c);
   if (rc) return rc;
   hipError_t e = hipStreamSynchronize(c->stream);
-  return e == hipSuccess ? MR_OK : hip_fail(c, e, "hipStreamSynchronize");
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  if (c->fused_used && c->scratch.sync) {
+    uint32_t word = 0;
+    uint32_t* dev = c->scratch.sync + mr::kSyncErrWord;
+    e = hipMemcpy(&word, dev, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "read fused error word");
+    if (word) {
+      const uint32_t zero = 0;
+      e = hipMemcpy(dev, &zero, 4, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return hip_fail(c, e, "reset fused error word");
+      return set_err(c, MR_E_LAUNCH, "fused decode kernel: a cross-workgroup wait ran out (results of that launch are invalid)");
+    }
+  }
+  return MR_OK;
 }
 
 int mr_dev_alloc(mr_ctx* c, uint64_t nbytes, void** out) {
@@ -558,8 +576,18 @@ int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
   if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, 1))) return rc;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u)
+    return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
   mr::Scratch& s = c->scratch;
-  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, 1, s.logits);
+  hipError_t e;
+  if (c->decode_kernel != MR_DECODE_VALU && mr::fused_supported(*L)) {
+    c->fused_used = true;
+    e = mr::launch_fused(c->launch(), *L, x, y, s.sync, static_cast<uint8_t*>(s.mfma_b), c->spin_limit);
+    return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
+  }
+  if (c->decode_kernel == MR_DECODE_MFMA)
+    return set_err(c, MR_E_UNSUPPORTED, "the fused MFMA decode kernel does not cover this layer shape");
+  e = mr::launch_router_logits(c->launch(), *L, x, 1, s.logits);
   if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
   if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, 1, s.idx, s.w, s.act, s.act_sh, y);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "moe forward launch");

@@ -83,6 +83,8 @@ struct mr_ctx {
   bool own_stream = false;
   int n_cu = 0;
   int decode_kernel = MR_DECODE_AUTO;
+  uint32_t spin_limit = 1u << 22;  // bounded waits of the fused kernel
+  bool fused_used = false;
   std::string err;
   mr::Scratch scratch;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -128,5 +130,11 @@ hipError_t launch_experts_valu(const Launch& K, const mr_layer& L, const float* 
                                float* y);
 hipError_t launch_dequant(const Launch& K, const mr_pack& p, uint32_t expert, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+
+// Fused single-launch MXFP4 decode layer (mr_fused.hip).
+constexpr int kSyncErrWord = 96;  // uint32 index of the fused kernel's error word
+bool fused_supported(const mr_layer& L);
+hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
+                        uint32_t* sync, uint8_t* img_base, uint32_t spin_limit);
 
 }  // namespace mr

@@ -26,6 +26,7 @@ ACT_SILU, ACT_SWIGLU_OAI = 0, 1
 DEVICE_NONE = -1
 OPT_DECODE_KERNEL = 1
 OPT_PROFILE = 2
+OPT_SPIN_LIMIT = 3
 DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 
 if not LIB_PATH.exists():

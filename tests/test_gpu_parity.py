@@ -231,3 +231,104 @@ def test_graph_replay_matches_eager(gpu_ctx, layers):
     g.close()
     for b in (dx, dy_e, dy_g):
         b.free()
+
+
+# ---- fused single-launch MXFP4 decode kernel -----------------------------------------
+
+@pytest.mark.parametrize("name", ["tiny-mxfp4", "C1-gpt-oss"])
+def test_fused_matches_oracle_and_valu(gpu_ctx, layers, name):
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    L = oracle.layer_from_host(host)
+    x = W.x_tokens(spec, 4, first_token=40)
+    dx = gpu_ctx.to_device(x)
+    dy = gpu_ctx.alloc(spec.hidden * 4)
+    try:
+        for t in range(4):
+            xp = dx.ptr + t * spec.hidden * 4
+            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_MFMA)
+            dl.layer.forward(xp, dy)
+            gpu_ctx.sync()
+            yf = dy.download(np.float32)
+            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_VALU)
+            dl.layer.forward(xp, dy)
+            yv = dy.download(np.float32)
+            ry, ridx, _, rlg = L.forward(x[t])
+            s = np.sort(rlg[0])[::-1]
+            if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg).max():
+                assert rel_err(yf, ry[0]) <= REL_TOL, (t, rel_err(yf, ry[0]))
+                assert rel_err(yf, yv) <= 2 * REL_TOL
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+    dx.free(), dy.free()
+
+
+def test_fused_repeated_launches_are_identical(gpu_ctx, layers):
+    dl, _ = get_layer(gpu_ctx, layers, "C1-gpt-oss")
+    spec = dl.spec
+    x = W.x_tokens(spec, 2, first_token=60)
+    dx0, dx1 = gpu_ctx.to_device(x[0]), gpu_ctx.to_device(x[1])
+    ys = [gpu_ctx.alloc(spec.hidden * 4) for _ in range(3)]
+    dl.layer.forward(dx0, ys[0])
+    dl.layer.forward(dx1, ys[1])
+    ref0, ref1 = ys[0].download(np.float32), ys[1].download(np.float32)
+    for rep in range(40):  # alternating inputs: every launch starts from the previous one's sync words
+        dl.layer.forward(dx0 if rep % 2 == 0 else dx1, ys[2])
+        got = ys[2].download(np.float32)
+        assert np.array_equal(got, ref0 if rep % 2 == 0 else ref1), rep
+    gpu_ctx.sync()
+    for b in ys + [dx0, dx1]:
+        b.free()
+
+
+def test_fused_graph_replay(gpu_ctx, layers):
+    dl, _ = get_layer(gpu_ctx, layers, "tiny-mxfp4")
+    spec = dl.spec
+    dl.layer.reserve(1)
+    x = W.x_tokens(spec, 1, first_token=70)
+    dx = gpu_ctx.to_device(x[0])
+    dy_e, dy_g = gpu_ctx.alloc(spec.hidden * 4), gpu_ctx.alloc(spec.hidden * 4)
+    dl.layer.forward(dx, dy_e)
+    eager = dy_e.download(np.float32)
+    gpu_ctx.graph_begin()
+    dl.layer.forward(dx, dy_g)
+    dl.layer.forward(dx, dy_g)  # two launches per replay: the epoch advances inside the graph
+    g = gpu_ctx.graph_end()
+    for rep in range(5):
+        gpu_ctx.check(M.lib.mr_dev_zero(gpu_ctx.h, dy_g.ptr, spec.hidden * 4))
+        g.launch()
+        dl.layer.forward(dx, dy_e)
+        gpu_ctx.sync()
+        assert np.array_equal(dy_g.download(np.float32), eager), rep
+    g.close()
+    for b in (dx, dy_e, dy_g):
+        b.free()
+
+
+def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers):
+    """A tiny spin limit (forced from the host) may make a cross-workgroup wait
+    run out: the kernel still exits, mr_sync reports it, and the next launch
+    with the default limit is correct."""
+    dl, host = get_layer(gpu_ctx, layers, "C1-gpt-oss")
+    spec = dl.spec
+    x = W.x_tokens(spec, 1, first_token=80)
+    dx, dy = gpu_ctx.to_device(x[0]), gpu_ctx.alloc(spec.hidden * 4)
+    dl.layer.forward(dx, dy)
+    ref = dy.download(np.float32)
+    gpu_ctx.set_option(M.OPT_SPIN_LIMIT, 1)
+    errors = 0
+    try:
+        for _ in range(5):
+            dl.layer.forward(dx, dy)
+            try:
+                gpu_ctx.sync()
+            except M.MoeRocmError as e:
+                assert e.status == M.MR_E_LAUNCH and "wait ran out" in e.message
+                errors += 1
+    finally:
+        gpu_ctx.set_option(M.OPT_SPIN_LIMIT, 0)
+    dl.layer.forward(dx, dy)
+    gpu_ctx.sync()
+    assert np.array_equal(dy.download(np.float32), ref)
+    print(f"forced-timeout launches reporting an error: {errors} of 5")
+    dx.free(), dy.free()
