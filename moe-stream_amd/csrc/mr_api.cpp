@@ -114,7 +114,7 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   // MFMA B-operand images: x split (H/32 blocks) and act split (k*I/32 blocks),
   // 16 columns x 33 bytes per block, rounded generously.
   p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40);
-  p.sync = o, o += align_up(4096 + E * 64);
+  p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
   p.total = o;
   return p;
@@ -509,11 +509,32 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   L->ctx = c;
   L->d = *d;
   L->H = H, L->I = I, L->E = E, L->Ish = Ish, L->type = type;
+  if (has_dev(c) && mr::fused_supported(*L, c->n_cu)) {
+    // sync block of the fused decode kernel: counters start at zero
+    int rc = bind(c);
+    void* fs = nullptr;
+    hipError_t e = rc ? hipSuccess : hipMalloc(&fs, mr::fused_layer_sync_bytes());
+    if (!rc && e == hipSuccess) e = hipMemset(fs, 0, mr::fused_layer_sync_bytes());
+    if (rc || e != hipSuccess) {
+      if (fs) (void)hipFree(fs);
+      delete L;
+      return rc ? rc : hip_fail(c, e, "hipMalloc(fused sync)");
+    }
+    L->fused_sync = static_cast<uint32_t*>(fs);
+  }
   *res = L;
   return MR_OK;
 }
 
-void mr_layer_destroy(mr_layer* L) { delete L; }
+void mr_layer_destroy(mr_layer* L) {
+  if (!L) return;
+  if (L->fused_sync && has_dev(L->ctx)) {
+    (void)bind(L->ctx);
+    (void)hipStreamSynchronize(L->ctx->stream);
+    (void)hipFree(L->fused_sync);
+  }
+  delete L;
+}
 
 int mr_reserve(mr_ctx* c, const mr_layer* L, uint32_t max_tokens) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
@@ -580,9 +601,9 @@ int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
     return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
   mr::Scratch& s = c->scratch;
   hipError_t e;
-  if (c->decode_kernel != MR_DECODE_VALU && mr::fused_supported(*L)) {
+  if (c->decode_kernel != MR_DECODE_VALU && L->fused_sync && mr::fused_supported(*L, c->n_cu)) {
     c->fused_used = true;
-    e = mr::launch_fused(c->launch(), *L, x, y, s.sync, static_cast<uint8_t*>(s.mfma_b), c->spin_limit);
+    e = mr::launch_fused(c->launch(), *L, x, y, s.sync + mr::kSyncErrWord, static_cast<uint8_t*>(s.mfma_b), c->spin_limit, c->n_cu);
     return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
   }
   if (c->decode_kernel == MR_DECODE_MFMA)

@@ -10,22 +10,36 @@
 // scale (GGUF kvalue*2^(e-128) == OCP e2m1*2^(e-127)). The activation vector is
 // the B operand, split into kTerms e4m3 terms (B columns 0..kTerms-1, each with
 // its own e8m0 scale per 32-element block); the column sum of D is the matvec.
-// K inside a block is ordered so that MFMA k=2j <-> GGUF element j and
-// k=2j+1 <-> element j+16 (byte j holds both), so no weight is repacked.
+// Within a block, MFMA k=2j <-> GGUF element j and k=2j+1 <-> element j+16
+// (byte j holds both), so no weight byte is moved or repacked.
 //
-// Work is split into three groups of workgroups in one grid, producers first:
-//   [0, R)        router: 4 experts per WG (one wave each) + the x split for
-//                 a share of the 32-element blocks; each wave publishes its
-//                 logit as a 64-bit (epoch+1, bits) word.
-//   [R, R+NG)     gate/up: 32 rows of one routed slot, both projections;
-//                 4 waves = 2 row tiles x 2 K halves. Epilogue: bias, SwiGLU,
-//                 * routing weight, split into the down projection's B image.
-//   [R+NG, grid)  down: 16 output rows; wave w takes slots w, w+4, ... Its down
-//                 weights are loaded into registers before the gate/up results
-//                 exist, so their HBM traffic overlaps the gate/up phase.
-// Cross-workgroup data moves through agent-coherent (sc1) loads and stores,
-// ordered by s_waitcnt; every wait is bounded (kSpinLimit) and a timeout sets
-// an error word the host reads at mr_sync, so no launch can hang.
+// Operand layout of the 16x16x128 f8f6f4 MFMA on gfx950 (lane = 16*g + i):
+//   A (fp4): row i, K [32g, 32g+32), nibble n (byte n/2, low nibble first) = K 32g+n;
+//            scale_a = e8m0 of that 32-K block.
+//   B (fp8): column i, bytes 0..15 = K [16g, 16g+16), bytes 16..31 = K [64+16g, +16);
+//            scale_b of lane (i, g) applies to K block g = K [32g, 32g+32).
+//   D:       D[4g + r][i] in element r.
+//
+// Three groups of workgroups share one grid:
+//   [0, R)        router: one expert logit per wave; publishes the logit and
+//                 bumps a counter.
+//   [R, R+ND)     down: 16 output rows; wave w takes routed slot w (top_k <= 4).
+//                 Its down weights are loaded into registers before the gate/up
+//                 results exist, so their HBM traffic overlaps the gate/up phase.
+//   [R+ND, grid)  gate/up: 32 rows of one routed slot, both projections; 4
+//                 waves = (gate, up) x 2 row tiles, each over the full K. The x
+//                 split is built in LDS while the router runs. Epilogue: bias,
+//                 SwiGLU, x routing weight, split into the down B image.
+// Workgroups are dispatched in index order; fused_supported keeps R + ND below
+// the CU count and the whole grid within 3 workgroups per CU (143 VGPRs, about
+// 50 KB LDS each), so every workgroup is resident from the start and no wait
+// can depend on a workgroup that has not been dispatched.
+// Small cross-workgroup values (logits, counters, the down B image) are written
+// with agent-coherent stores ordered by s_waitcnt; the down workgroups read the
+// image through L2 after one agent-scope acquire. Every wait is bounded (the
+// context's spin limit); a wait that runs out sets an error word read at
+// mr_sync and the launch still exits. The last workgroup to finish resets the
+// counters for the next launch.
 #include "mr_device.h"
 #include "mr_internal.h"
 
@@ -33,16 +47,29 @@
 
 namespace mr {
 
-constexpr int kTerms = 4;        // e4m3 terms of an activation split (B columns used)
-constexpr int kGuSteps = 12;     // K steps (4 blocks each) per gate/up wave: H <= 3072
-constexpr int kDnSteps = 23;     // K steps per down wave: I <= 2944
+constexpr int kTerms = 4;               // e4m3 terms of an activation split (B columns used)
+constexpr int kSteps = 23;              // K steps (4 blocks each) per wave: H, I <= 2944
+constexpr int kRouterVec = 12;          // float4 pairs per lane of a router row: H <= 3072
+constexpr int kImgVec = 12;             // 16-byte image loads per lane for one slot: I <= 3072
 constexpr int kImgBytes = kTerms * 32;  // B image bytes per 32-element block
-constexpr int kRouterVec = 12;  // float4 per lane of a router row: H <= 3072
-constexpr int kSplitRounds = 12; // split blocks per half-wave of a router WG
-constexpr int kImgRegs = 6;      // x image u64 words per thread: H <= 3072
 
-// sync words (uint32 indices into Scratch::sync); tags start at byte 512
-enum : int { SW_EPOCH = 0, SW_GU_DONE = 32, SW_WG_DONE = 64, SW_ERR = 96, SW_TAG0 = 128 };
+// Per-layer sync block (uint32 words, zeroed once at layer creation). The
+// counters only grow: launch n of a layer waits for (n+1)*E logits and
+// (n+1)*NG gate/up units, so nothing has to be reset between launches. The
+// producer counters are spread over kCopies lines (copy = producer id % kCopies)
+// and incremented without waiting for a return value; a waiter sums the copies.
+constexpr int kCopies = 8;
+enum : int {
+  FS_SEQ = 0,       // launches completed (advanced by the last down workgroup)
+  FS_DN = 32,       // down workgroups finished (returning atomic)
+  FS_ROUTE = 256,   // [kCopies] x 64 words: logits published
+  FS_GU = 768,      // [kCopies] x 64 words: gate/up units finished
+  FS_LOGITS = 1280  // [E] logits of the current launch
+};
+constexpr int kLayerSyncWords = FS_LOGITS + 512;
+constexpr int kRouteLdsOff = 32768;  // byte offset of the routing scratch in dynamic LDS
+static_assert(96 * kImgBytes <= kRouteLdsOff && kRouteLdsOff + 512 * 4 <= 4 * kImgVec * 1024,
+              "routing scratch must clear the x image and fit in the slot images");
 
 struct FusedArgs {
   const uint8_t* gate;
@@ -59,259 +86,251 @@ struct FusedArgs {
   const float* mask;
   const float* x;
   float* y;
-  uint32_t* sync;
-  uint8_t* ximg;    // [nbH][kImgBytes] x split image
-  uint32_t* xsc;    // [nbH] 4 e8m0 bytes (one per term)
-  uint8_t* dimg;    // [k][nbI][kImgBytes] down B image
-  uint32_t* dsc;    // [k][nbI]
+  uint32_t* fs;   // this layer's sync block
+  uint32_t* err;  // context error word (read and cleared by mr_sync)
+  uint8_t* dimg;  // [k][nbI][kImgBytes] down B image
+  uint32_t* dsc;  // [k][nbI] 4 e8m0 bytes (one per term)
   int H, I, E, k;
   uint32_t flags;
   int act;
   float alpha, limit;
   int R, NG, ND;
   uint32_t spin_limit;
-  uint32_t lds_img_bytes;  // dynamic LDS: image bytes, then 4-byte scales
+  uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
+  unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][8] timestamps
 };
 
-// ---- agent-coherent accesses (global_load/store ... sc1) ----------------------
-__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef MR_FUSED_TRACE
+#define TRACE(slot)                                                                       \
+  do {                                                                                    \
+    if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 8 + (slot)] = wall_clock64(); \
+  } while (0)
+#else
+#define TRACE(slot) \
+  do {              \
+  } while (0)
+#endif
+
+// ---- DPP ---------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ unsigned long long ld_sc1(const unsigned long long* p) {
+constexpr int kDppXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppHMirror = 0x141;  // row_half_mirror: lane i <-> 7-i within 8
+
+// max over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  return fmaxf(v, dpp_f<kDppHMirror>(v));
+}
+// sum over each quad, in every lane of the quad
+__device__ __forceinline__ float sum4(float v) {
+  v += dpp_f<kDppXor1>(v);
+  return v + dpp_f<kDppXor2>(v);
+}
+
+// ---- agent-coherent accesses (global_load/store ... sc1) ---------------------------
+__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_sc1(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_sc1(unsigned long long* p, unsigned long long v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint32_t add_sc1(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// All vector memory operations of this wave issued so far have completed.
+// All vector memory operations this wave has issued have completed.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// ---- DPP reductions ------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+// Count one finished producer (no return value is waited for).
+__device__ __forceinline__ void count(uint32_t* copies, int id) {
+  (void)__hip_atomic_fetch_add(copies + 64 * (id % kCopies), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
 }
-#define DPP_XOR1 0xB1      // quad_perm [1,0,3,2]
-#define DPP_XOR2 0x4E      // quad_perm [2,3,0,1]
-#define DPP_HMIRROR 0x141  // row_half_mirror
-#define DPP_MIRROR 0x140   // row_mirror
+// Bounded wait (one wave) until the counter copies sum to at least `target`
+// (wrap-around safe); false if the limit ran out.
+__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
+  const int lane = threadIdx.x & 63;
+  for (uint32_t it = 0;; ++it) {
+    uint32_t c = lane < kCopies ? ld_sc1(copies + 64 * lane) : 0u;
+    // sum of kCopies (= 8) lanes: exact in uint32 via two 16-bit halves in floats
+    float lo = (float)(c & 0xFFFFu), hi = (float)(c >> 16);
+    lo += dpp_f<kDppXor1>(lo), hi += dpp_f<kDppXor1>(hi);
+    lo += dpp_f<kDppXor2>(lo), hi += dpp_f<kDppXor2>(hi);
+    lo += dpp_f<kDppHMirror>(lo), hi += dpp_f<kDppHMirror>(hi);
+    const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)lo + ((uint32_t)hi << 16)));
+    if ((int32_t)(sum - target) >= 0) return true;
+    if (it >= limit) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
 
-// max over each aligned group of 32 lanes, result in every lane of the group
-__device__ __forceinline__ float max32(float v) {
-  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
-  v = fmaxf(v, dpp_f<DPP_XOR2>(v));
-  v = fmaxf(v, dpp_f<DPP_HMIRROR>(v));
-  v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
-  return fmaxf(v, __shfl_xor(v, 16, 64));
-}
-// sum over each quad (lanes 4m..4m+3), result in every lane of the quad
-__device__ __forceinline__ float sum4(float v) {
-  v += dpp_f<DPP_XOR1>(v);
-  return v + dpp_f<DPP_XOR2>(v);
+// ---- e4m3 activation split -----------------------------------------------------------
+// One 32-element block is held by 8 lanes; lane m holds MFMA positions
+// 4m..4m+3 = GGUF elements 2m, 2m+16, 2m+1, 2m+17 of the block.
+// Term t: scale 2^(floor(log2 max|r_t|) - 7) so max|r_t|/scale is in [128, 256);
+// codes by v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even); the residual
+// after kTerms terms is below 2^-16 of the block max. codes[t] is the code
+// dword of term t; the kTerms scale bytes are packed into `scales`.
+__device__ __forceinline__ void split_block8(float v0, float v1, float v2, float v3,
+                                             uint32_t codes[kTerms], uint32_t& scales) {
+  float r0 = v0, r1 = v1, r2 = v2, r3 = v3;
+  scales = 0u;
+#pragma unroll
+  for (int t = 0; t < kTerms; ++t) {
+    const float m = max8(fmaxf(fmaxf(fabsf(r0), fabsf(r1)), fmaxf(fabsf(r2), fabsf(r3))));
+    const int ex = (int)((__float_as_uint(m) >> 23) & 0xFFu);  // biased exponent; 0: zero/denormal
+    const int sb = ex - 7;                                     // e8m0 byte of 2^(e-7)
+    uint32_t c = 0u;
+    if (sb > 0) {
+      const float inv = __uint_as_float((uint32_t)(254 - sb) << 23);  // 2^-(e-7)
+      const float sc = __uint_as_float((uint32_t)sb << 23);           // 2^(e-7)
+      c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
+      c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r2 * inv, r3 * inv, (int)c, true);
+      const f32x2 d01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c, false);
+      const f32x2 d23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c, true);
+      r0 -= d01.x * sc, r1 -= d01.y * sc, r2 -= d23.x * sc, r3 -= d23.y * sc;
+      scales |= (uint32_t)sb << (8 * t);
+    }
+    codes[t] = c;
+  }
 }
 
-// ---- e4m3 activation split ---------------------------------------------------------
-// OCP e4m3 (bias 7) code of v, |v| < 256, round to nearest even; dec = its value.
-__device__ __forceinline__ uint32_t e4m3_rne(float v, float& dec) {
-  const float a = fabsf(v);
-  uint32_t code;
-  if (a < 0.015625f) {  // subnormal range: multiples of 2^-9
-    const float q = rintf(a * 512.0f);
-    code = (uint32_t)q;
-    dec = q * (1.0f / 512.0f);
+// ---- operands ----------------------------------------------------------------------------
+// B operand of lane (col i, group g) for K step st from a B image in LDS.
+// Columns i >= kTerms and blocks past nb read `zero` (32 zero bytes in LDS),
+// so the loads need no per-lane branches.
+__device__ __forceinline__ void load_b(const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
+                                       int st, int nb, int i, int g, i32x8& B, int& sb) {
+  const bool col = i < kTerms;
+  const int b0 = 4 * st + (g >> 1), b1 = b0 + 2, off = i * 32 + 16 * (g & 1);
+  const uint8_t* p0 = (col && b0 < nb) ? img + (size_t)b0 * kImgBytes + off : zero;
+  const uint8_t* p1 = (col && b1 < nb) ? img + (size_t)b1 * kImgBytes + off : zero;
+  const i32x4 v0 = *reinterpret_cast<const i32x4*>(p0);
+  const i32x4 v1 = *reinterpret_cast<const i32x4*>(p1);
+  B = i32x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  const int bs = min(4 * st + g, nb - 1);
+  sb = col ? (int)((sc[bs] >> (8 * (i & 3))) & 0xFFu) : 127;
+}
+
+// Raw 20-byte window (5 aligned dwords) holding one 17-byte block.
+struct RawBlk {
+  uint32_t d[5];
+};
+__device__ __forceinline__ void raw_load(const uint8_t* p, RawBlk& r) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
+  r.d[0] = w[0], r.d[1] = w[1], r.d[2] = w[2], r.d[3] = w[3], r.d[4] = w[4];
+}
+__device__ __forceinline__ void raw_zero(RawBlk& r) { r.d[0] = r.d[1] = r.d[2] = r.d[3] = r.d[4] = 0u; }
+
+// One MFMA on a raw block window; sh = block address & 3. The 16 code bytes
+// start at byte sh+1 of the window.
+__device__ __forceinline__ f32x4 mfma_raw(const RawBlk& r, uint32_t sh, bool valid, const i32x8& B,
+                                          int sb, f32x4 acc) {
+  const uint32_t t = sh + 1u;
+  uint32_t q0, q1, q2, q3;
+  if (t == 4u) {
+    q0 = r.d[1], q1 = r.d[2], q2 = r.d[3], q3 = r.d[4];
   } else {
-    const uint32_t b = __float_as_uint(a);
-    const uint32_t r = (b + 0x7FFFFu + ((b >> 20) & 1u)) & ~0xFFFFFu;
-    dec = __uint_as_float(r);
-    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    q0 = __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
+    q1 = __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
+    q2 = __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
+    q3 = __builtin_amdgcn_alignbyte(r.d[4], r.d[3], t);
   }
-  if (v < 0.0f) {
-    dec = -dec;
-    code |= 0x80u;
-  }
-  return code;
+  const int sa = valid ? (int)((r.d[0] >> (8u * sh)) & 0xFFu) : 127;
+  const i32x8 A = {(int)q0, (int)q1, (int)q2, (int)q3, 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
 }
 
-// Split one 32-element block held one element per lane (32-lane group, lane p
-// holds MFMA position p) into kTerms e4m3 terms. Term t uses the scale
-// 2^(floor(log2(max|r_t|)) - 7), so max|r_t|/scale is in [128, 256) and each
-// term adds 4 bits; the residual after the terms is below 2^-16 of the block max.
-// Returns the 4 codes packed (term t in byte t) and the 4 scale bytes likewise.
-__device__ __forceinline__ void split32(float v, uint32_t& codes, uint32_t& scales) {
-  float r = v;
-  codes = 0u, scales = 0u;
+// D += sum over the K steps of one 16-row tile: A from raw windows `rw`, B from
+// a B image in LDS.
+__device__ __forceinline__ f32x4 mfma_chain(const RawBlk (&rw)[kSteps], uint32_t sh, int S, int nb,
+                                            const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
+                                            int i, int g, f32x4 acc) {
 #pragma unroll
-  for (int t = 0; t < kTerms; ++t) {
-    const float m = max32(fabsf(r));
-    const int e = (int)((__float_as_uint(m) >> 23) & 0xFFu) - 127;  // m == 0 -> e = -127
-    const int sb = e + 120;  // e8m0 byte of 2^(e-7)
-    uint32_t code = 0u;
-    float dec = 0.0f;
-    if (sb > 0 && m > 0.0f) {
-      code = e4m3_rne(r * __uint_as_float((uint32_t)(254 - sb) << 23), dec);  // r * 2^-(e-7)
-      dec = dec * __uint_as_float((uint32_t)sb << 23);                        // * 2^(e-7)
+  for (int j = 0; j < kSteps; ++j) {
+    if (j < S) {
+      i32x8 B;
+      int sb;
+      load_b(img, sc, zero, j, nb, i, g, B, sb);
+      const int c = 4 * j + g;
+      acc = mfma_raw(rw[j], (sh + (uint32_t)min(c, nb - 1)) & 3u, c < nb, B, sb, acc);
     }
-    r -= dec;
-    codes |= code << (8 * t);
-    scales |= (uint32_t)(sb > 0 && m > 0.0f ? sb : 0) << (8 * t);
   }
+  return acc;
 }
 
-// Gather byte t of `codes` from the 4 lanes of each quad into one dword (in the
-// quad's first lane): bytes of positions 4m..4m+3 of term t.
-__device__ __forceinline__ uint32_t quad_pack(uint32_t codes, int t) {
-  uint32_t b = (codes >> (8 * t)) & 0xFFu;
+// ---- routing ----------------------------------------------------------------------------
+// Wave 0 of a consumer workgroup: wait until every logit of this launch is
+// published, then select the top-k (largest first, ties to the lower index;
+// top_k_routing layer.rs:2346-2403) by ranking each expert against all others
+// in LDS, and write slot -> (expert, weight) to LDS.
+__device__ bool route_wave(const FusedArgs& a, uint32_t seq, int* sel_i, float* sel_w,
+                           float* lds_v) {
   const int lane = threadIdx.x & 63;
-  uint32_t b1 = __shfl(b, lane + 1, 64), b2 = __shfl(b, lane + 2, 64), b3 = __shfl(b, lane + 3, 64);
-  return b | (b1 << 8) | (b2 << 16) | (b3 << 24);
-}
-
-// Split the 32-element block at lanes [32h, 32h+32) of the wave and store its
-// image with sc1 dword stores: img[t*32 + p] = code of position p, term t.
-__device__ __forceinline__ void split_store(float v, uint8_t* img, uint32_t* sc, bool active) {
-  uint32_t codes, scales;
-  split32(v, codes, scales);
-  const int p = threadIdx.x & 31;
-#pragma unroll
-  for (int t = 0; t < kTerms; ++t) {
-    const uint32_t dw = quad_pack(codes, t);
-    if (active && (p & 3) == 0) st_sc1(reinterpret_cast<uint32_t*>(img + t * 32 + p), dw);
-  }
-  if (active && p == 0) st_sc1(sc, scales);
-}
-
-// ---- operands ------------------------------------------------------------------
-// B operand of lane (col i, group g) for K step st from a B image in LDS:
-// data bytes 0..15 = K [16g, 16g+16) = block 4st+g/2, half g&1; bytes 16..31 =
-// K [64+16g, ...) = block 4st+2+g/2; scale = block 4st+g (MFMA scale indexing).
-__device__ __forceinline__ void load_b(const uint8_t* img, const uint32_t* sc, int st, int nb,
-                                       int i, int g, i32x8& B, int& sb) {
-  B = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-  sb = 127;
-  if (i < kTerms) {
-    const int b0 = 4 * st + (g >> 1), b1 = b0 + 2, off = i * 32 + 16 * (g & 1);
-    if (b0 < nb) {
-      const i32x4 v = *reinterpret_cast<const i32x4*>(img + (size_t)b0 * kImgBytes + off);
-      B[0] = v[0], B[1] = v[1], B[2] = v[2], B[3] = v[3];
-    }
-    if (b1 < nb) {
-      const i32x4 v = *reinterpret_cast<const i32x4*>(img + (size_t)b1 * kImgBytes + off);
-      B[4] = v[0], B[5] = v[1], B[6] = v[2], B[7] = v[3];
-    }
-    const int bs = 4 * st + g;
-    if (bs < nb) sb = (int)((sc[bs] >> (8 * i)) & 0xFFu);
-  }
-}
-
-__device__ __forceinline__ f32x4 mfma_fp4(const uint32_t a[4], uint32_t sa, const i32x8& B, int sb,
-                                          f32x4 acc) {
-  const i32x8 A = {(int)a[0], (int)a[1], (int)a[2], (int)a[3], 0, 0, 0, 0};
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, (int)sa, 0, sb);
-}
-
-// ---- routing ---------------------------------------------------------------------
-// Wave 0 of a consumer workgroup: wait until every expert's logit of this
-// launch is published, then select the top-k (same rule as k_topk: largest
-// first, ties to the lower index) and write slot -> (expert, weight) to LDS.
-__device__ bool route_wave(const FusedArgs& a, uint32_t epoch, int* sel_i, float* sel_w) {
-  const int lane = threadIdx.x & 63;
-  const unsigned long long* tags = reinterpret_cast<const unsigned long long*>(a.sync + SW_TAG0);
-  const uint32_t want = epoch + 1u;
-  float v[8];
-  bool live[8];
-  uint32_t it = 0;
-  for (;;) {
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      live[j] = e < a.E;
-      v[j] = 0.f;
-      if (live[j]) {
-        const unsigned long long t = ld_sc1(tags + e);
-        ok = ok && (uint32_t)(t >> 32) == want;
-        v[j] = __uint_as_float((uint32_t)t);
-      }
-    }
-    if (__all(ok)) break;
-    if (++it > a.spin_limit) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
+  if (!wait_count(a.fs + FS_ROUTE, (seq + 1u) * (uint32_t)a.E, a.spin_limit)) return false;
+  for (int e = lane; e < a.E; e += 64) lds_v[e] = __uint_as_float(ld_sc1(a.fs + FS_LOGITS + e));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   const bool softmax_after = (a.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
-  if (!softmax_after) {
+  if (!softmax_after) {  // rank by probability: softmax over all experts first
     float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (live[j]) m = fmaxf(m, v[j]);
+    for (int e = lane; e < a.E; e += 64) m = fmaxf(m, lds_v[e]);
     m = wave_max(m);
     float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (live[j]) v[j] = __expf(v[j] - m), s += v[j];
+    for (int e = lane; e < a.E; e += 64) s += __expf(lds_v[e] - m);
     s = wave_sum(s);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (live[j]) v[j] = v[j] / s;
+    for (int e = lane; e < a.E; e += 64) lds_v[e] = __expf(lds_v[e] - m) / s;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
-  float selv = 0.f;
-  for (int r = 0; r < a.k; ++r) {
-    float bv = 0.f;
-    int bi = -1;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (live[j] && (bi < 0 || v[j] > bv)) bv = v[j], bi = lane + 64 * j;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
+  if (lane < a.k) sel_i[lane] = 0, sel_w[lane] = 0.f;  // in range even if a NaN breaks the ranks
+  for (int e = lane; e < a.E; e += 64) {
+    const float v = lds_v[e];
+    int r = 0;
+    for (int e2 = 0; e2 < a.E; ++e2) {
+      const float v2 = lds_v[e2];
+      r += (v2 > v || (v2 == v && e2 < e)) ? 1 : 0;
     }
-    if (bi >= 0 && (bi & 63) == lane) live[bi >> 6] = false;
-    if (lane == r) selv = bv;
-    if (lane == 0) sel_i[r] = bi;
+    if (r < a.k) sel_i[r] = e, sel_w[r] = v;
   }
-  // weights: lanes 0..k-1 hold the selected values, in selection order
-  const bool in = lane < a.k;
-  if (softmax_after) {
-    float m = wave_max(in ? selv : -INFINITY);
-    float ex = in ? __expf(selv - m) : 0.f;
-    float s = wave_sum(ex);
-    if (in) sel_w[lane] = ex / s;
-  } else if (a.flags & MR_ROUTE_NORM_TOPK) {
-    float s = wave_sum(in ? selv : 0.f);
-    if (in) sel_w[lane] = selv / s;
-  } else if (in) {
-    sel_w[lane] = selv;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) {  // weights over the k selected values, in selection order
+    if (softmax_after) {
+      float m = -INFINITY, s = 0.f;
+      for (int r = 0; r < a.k; ++r) m = fmaxf(m, sel_w[r]);
+      for (int r = 0; r < a.k; ++r) s = s + __expf(sel_w[r] - m);
+      for (int r = 0; r < a.k; ++r) sel_w[r] = __expf(sel_w[r] - m) / s;
+    } else if (a.flags & MR_ROUTE_NORM_TOPK) {
+      float s = 0.f;
+      for (int r = 0; r < a.k; ++r) s = s + sel_w[r];
+      for (int r = 0; r < a.k; ++r) sel_w[r] = sel_w[r] / s;
+    }
   }
   return true;
 }
 
-__device__ __forceinline__ void fail(const FusedArgs& a) { st_sc1(a.sync + SW_ERR, 1u); }
+__device__ __forceinline__ void fail(const FusedArgs& a) { st_sc1(a.err, 1u); }
 
-// A operands of one 16-row tile of a down matrix, all K steps.
-__device__ __forceinline__ void load_down_rows(const uint8_t* D, int S, int nbI, int g,
-                                               uint32_t (&ad)[kDnSteps][4], uint32_t (&sd)[kDnSteps]) {
+// A operands (raw windows) of one 16-row tile, all K steps (S is wave-uniform).
+// Blocks past the row end (last step, lane groups g beyond nb) load the row's
+// last block instead: their B operand is all zero, so they add exactly 0.
+__device__ __forceinline__ void issue_rows(const uint8_t* W, int S, int nb, int g,
+                                           RawBlk (&rw)[kSteps]) {
 #pragma unroll
-  for (int j = 0; j < kDnSteps; ++j) {
-    const int c = 4 * j + g;
-    if (j < S && c < nbI) {
-      mx_load_block(D + (size_t)c * 17, sd[j], ad[j]);
-    } else {
-      sd[j] = 127u;
-      ad[j][0] = ad[j][1] = ad[j][2] = ad[j][3] = 0u;
-    }
+  for (int j = 0; j < kSteps; ++j) {
+    if (j < S)
+      raw_load(W + (size_t)min(4 * j + g, nb - 1) * 17, rw[j]);
+    else
+      raw_zero(rw[j]);
   }
 }
 
-// ---- the kernel ------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_fused_mxfp4(FusedArgs a) {
-  extern __shared__ __align__(16) uint8_t lds_dyn[];  // x image (gate/up) or down images + scales
+// ---- the kernel ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
+  extern __shared__ __align__(16) uint8_t lds_dyn[];
   uint8_t* lds_img = lds_dyn;
   uint32_t* lds_sc = reinterpret_cast<uint32_t*>(lds_dyn + a.lds_img_bytes);
   __shared__ float lds_part[2 * 2 * 2 * 16];
@@ -319,150 +338,114 @@ __global__ __launch_bounds__(256) void k_fused_mxfp4(FusedArgs a) {
   __shared__ int sel_i[16];
   __shared__ float sel_w[16];
   __shared__ int ok_flag;
+  __shared__ __align__(16) uint8_t lds_zero[32];
+  // routing scratch: past the x image of gate/up workgroups (<= 12 KiB) and in
+  // the slot images of down workgroups, which are written only after routing
+  float* lds_route = reinterpret_cast<float*>(lds_img + kRouteLdsOff);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int bid = blockIdx.x;
-  const uint32_t epoch = ld_sc1(a.sync + SW_EPOCH);
   const int nbH = a.H >> 5, nbI = a.I >> 5;
+  TRACE(0);
+  const uint32_t seq = ld_sc1(a.fs + FS_SEQ);
+  if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
-    // Issue every load first: this wave's router row and x for the dot, and
-    // the x elements of this workgroup's share of the split blocks.
     const int e = bid * 4 + wave;
-    const bool has_e = e < a.E;
-    const float* wrow = a.router_w + (size_t)(has_e ? e : 0) * a.H;
-    f32x4 xr[kRouterVec], wr[kRouterVec];
+    if (e < a.E) {
+      const float* w = a.router_w + (size_t)e * a.H;
+      f32x4 xv[kRouterVec], wv[kRouterVec];  // every load issued before the first use
 #pragma unroll
-    for (int j = 0; j < kRouterVec; ++j) {
-      const int c = (lane + 64 * j) * 4;
-      if (has_e && c < a.H) {
-        xr[j] = *reinterpret_cast<const f32x4*>(a.x + c);
-        wr[j] = *reinterpret_cast<const f32x4*>(wrow + c);
-      } else {
-        xr[j] = f32x4{0.f, 0.f, 0.f, 0.f}, wr[j] = xr[j];
+      for (int j = 0; j < kRouterVec; ++j) {
+        const int c = (lane + 64 * j) * 4;
+        const bool in = c < a.H;
+        xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kRouterVec; ++j) {
+        acc = __builtin_fmaf(xv[j].x, wv[j].x, acc);
+        acc = __builtin_fmaf(xv[j].y, wv[j].y, acc);
+        acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
+        acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) {
+        if (a.router_b) acc = acc + a.router_b[e];
+        if (a.mask) acc = acc + a.mask[e];
+        st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
+        vm_drain();  // the logit is visible before the count that announces it
+        count(a.fs + FS_ROUTE, e);
       }
     }
-    const int bpw = (nbH + a.R - 1) / a.R;
-    const int half = lane >> 5, p = lane & 31;
-    const int elem = (p >> 1) + 16 * (p & 1);  // MFMA position p <-> GGUF element
-    float xs[kSplitRounds];
-#pragma unroll
-    for (int j = 0; j < kSplitRounds; ++j) {
-      const int jb = (wave * 2 + half) + 8 * j, b = bid * bpw + jb;
-      xs[j] = (jb < bpw && b < nbH) ? a.x[b * 32 + elem] : 0.f;
-    }
-    // x split of the share; stored before this workgroup publishes any logit,
-    // so a consumer that sees all logits also sees the whole x image
-#pragma unroll
-    for (int j = 0; j < kSplitRounds; ++j) {
-      const int jb0 = wave * 2 + 8 * j;  // first half-wave's block of this round
-      if (jb0 < bpw) {
-        const int jb = jb0 + half, b = bid * bpw + jb;
-        const bool act = jb < bpw && b < nbH;
-        split_store(xs[j], a.ximg + (size_t)(act ? b : 0) * kImgBytes, a.xsc + (act ? b : 0), act);
-      }
-    }
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < kRouterVec; ++j) {
-      acc = __builtin_fmaf(xr[j].x, wr[j].x, acc);
-      acc = __builtin_fmaf(xr[j].y, wr[j].y, acc);
-      acc = __builtin_fmaf(xr[j].z, wr[j].z, acc);
-      acc = __builtin_fmaf(xr[j].w, wr[j].w, acc);
-    }
-    acc = wave_sum(acc);
-    vm_drain();       // this wave's split stores are complete ...
-    __syncthreads();  // ... and so are those of the other waves
-    if (has_e && lane == 0) {
-      if (a.router_b) acc = acc + a.router_b[e];
-      if (a.mask) acc = acc + a.mask[e];
-      st_sc1(reinterpret_cast<unsigned long long*>(a.sync + SW_TAG0) + e,
-             ((unsigned long long)(epoch + 1u) << 32) | __float_as_uint(acc));
-    }
-  } else if (bid < a.R + a.NG) {
+    TRACE(1);
+  } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
-    const int gid = bid - a.R;
+    const int gid = bid - a.R - a.ND;
     const int nrp = a.I >> 5;
-    const int slot = gid / nrp, pair = gid % nrp;
+    // x split image in LDS (independent of routing): 8 lanes per block, all
+    // loads issued first
+    {
+      constexpr int kRounds = 3;  // 96 blocks / 32 per pass: H <= 3072
+      const int m = tid & 7;
+      f32x2 lo[kRounds], hi[kRounds];
+#pragma unroll
+      for (int j = 0; j < kRounds; ++j) {
+        const int b = (tid >> 3) + 32 * j;
+        const float* xb = a.x + b * 32 + 2 * m;
+        lo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb) : f32x2{0.f, 0.f};        // 2m, 2m+1
+        hi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb + 16) : f32x2{0.f, 0.f};   // 2m+16, 2m+17
+      }
+#pragma unroll
+      for (int j = 0; j < kRounds; ++j) {
+        const int b = (tid >> 3) + 32 * j;
+        if (b < nbH) {
+          uint32_t codes[kTerms], scales;
+          split_block8(lo[j].x, hi[j].x, lo[j].y, hi[j].y, codes, scales);
+#pragma unroll
+          for (int t = 0; t < kTerms; ++t)
+            *reinterpret_cast<uint32_t*>(lds_img + (size_t)b * kImgBytes + t * 32 + 4 * m) = codes[t];
+          if (m == 0) lds_sc[b] = scales;
+        }
+      }
+    }
+    TRACE(1);
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(a, epoch, sel_i, sel_w)) {
+    if (wave == 0 && !route_wave(a, seq, sel_i, sel_w, lds_route)) {
       if (lane == 0) ok_flag = 0, fail(a);
     }
-    __syncthreads();
-    if (ok_flag) {
+    __syncthreads();  // routing and x image ready
+    TRACE(2);
+    if (ok_flag && gid < a.NG) {  // one unit per workgroup
+      const int unit = gid;
+      const int slot = unit / nrp, pair = unit % nrp;
       const int e = sel_i[slot];
       const float wsl = sel_w[slot];
-      // x split image (complete once every logit is published): issue its
-      // loads first, then the weight loads, then move the image to LDS
-      const int n8 = nbH * kImgBytes / 8;
-      const unsigned long long* xsrc = reinterpret_cast<const unsigned long long*>(a.ximg);
-      unsigned long long ximg[kImgRegs];
-      uint32_t xscr = 0u;
-#pragma unroll
-      for (int j = 0; j < kImgRegs; ++j) {
-        const int idx = tid + 256 * j;
-        ximg[j] = idx < n8 ? ld_sc1(xsrc + idx) : 0ull;
-      }
-      if (tid < nbH) xscr = ld_sc1(a.xsc + tid);
-      const int tile = wave & 1, kh = wave >> 1;
-      const int S = (nbH + 3) >> 2, S0 = (S + 1) >> 1;
-      const int st0 = kh * S0, nst = min(S0, S - st0);
+      const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
+      const int S = (nbH + 3) >> 2;
       const int row = pair * 32 + tile * 16 + i;
       const uint64_t rb = (uint64_t)nbH * 17;
-      const uint8_t* G = a.gate + a.gate_off[e] + (uint64_t)row * rb;
-      const uint8_t* U = a.up + a.up_off[e] + (uint64_t)row * rb;
-      uint32_t ag[kGuSteps][4], au[kGuSteps][4], sg[kGuSteps], su[kGuSteps];
-#pragma unroll
-      for (int j = 0; j < kGuSteps; ++j) {
-        const int c = 4 * (st0 + j) + g;
-        if (j < nst && c < nbH) {
-          mx_load_block(G + (size_t)c * 17, sg[j], ag[j]);
-          mx_load_block(U + (size_t)c * 17, su[j], au[j]);
-        } else {
-          sg[j] = su[j] = 127u;
-          ag[j][0] = ag[j][1] = ag[j][2] = ag[j][3] = 0u;
-          au[j][0] = au[j][1] = au[j][2] = au[j][3] = 0u;
-        }
-      }
-      {
-        unsigned long long* dst = reinterpret_cast<unsigned long long*>(lds_img);
-#pragma unroll
-        for (int j = 0; j < kImgRegs; ++j) {
-          const int idx = tid + 256 * j;
-          if (idx < n8) dst[idx] = ximg[j];
-        }
-        if (tid < nbH) lds_sc[tid] = xscr;
-      }
-      __syncthreads();  // x image in LDS
-      f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < kGuSteps; ++j) {
-        if (j < nst) {
-          i32x8 B;
-          int sb;
-          load_b(lds_img, lds_sc, st0 + j, nbH, i, g, B, sb);
-          dg = mfma_fp4(ag[j], sg[j], B, sb, dg);
-          du = mfma_fp4(au[j], su[j], B, sb, du);
-        }
-      }
+      const uint8_t* W = (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]) + (uint64_t)row * rb;
+      const uint32_t shw = (uint32_t)reinterpret_cast<uintptr_t>(W) & 3u;
+      RawBlk rw[kSteps];
+      issue_rows(W, S, nbH, g, rw);
+      f32x4 dacc = mfma_chain(rw, shw, S, nbH, lds_img, lds_sc, lds_zero, i, g, f32x4{0.f, 0.f, 0.f, 0.f});
+      TRACE(3);
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float gs = sum4(dg[r]), us = sum4(du[r]);
-        if (i == 0) {
-          lds_part[((kh * 2 + tile) * 2 + 0) * 16 + 4 * g + r] = gs;
-          lds_part[((kh * 2 + tile) * 2 + 1) * 16 + 4 * g + r] = us;
-        }
+        const float cs = sum4(dacc[r]);
+        if (i == 0) lds_part[(mat * 2 + tile) * 16 + 4 * g + r] = cs;
       }
       __syncthreads();
       if (wave == 0) {
-        // lanes 0..31: rows pair*32 + lane; bias, SwiGLU, routing weight
-        if (lane < 32) {
+        if (lane < 32) {  // rows pair*32 + lane: bias, SwiGLU, routing weight
           const int t2 = lane >> 4, r16 = lane & 15;
-          float gv = lds_part[((0 * 2 + t2) * 2 + 0) * 16 + r16] + lds_part[((1 * 2 + t2) * 2 + 0) * 16 + r16];
-          float uv = lds_part[((0 * 2 + t2) * 2 + 1) * 16 + r16] + lds_part[((1 * 2 + t2) * 2 + 1) * 16 + r16];
+          float gv = lds_part[(0 * 2 + t2) * 16 + r16];
+          float uv = lds_part[(1 * 2 + t2) * 16 + r16];
           const int rr = pair * 32 + lane;
           if (a.gate_b) gv = gv + a.gate_b[(size_t)e * a.I + rr];
           if (a.up_b) uv = uv + a.up_b[(size_t)e * a.I + rr];
@@ -470,64 +453,74 @@ __global__ __launch_bounds__(256) void k_fused_mxfp4(FusedArgs a) {
           lds_act[lane] = h * wsl;
         }
         __builtin_amdgcn_wave_barrier();
-        const int p = lane & 31;
-        const float v = lds_act[(p >> 1) + 16 * (p & 1)];
-        const size_t blk = (size_t)slot * nbI + pair;
-        split_store(v, a.dimg + blk * kImgBytes, a.dsc + blk, lane < 32);
-        vm_drain();
-        if (lane == 0) add_sc1(a.sync + SW_GU_DONE, 1u);
+        if (lane < 8) {  // split the 32 values: one 32-element block of the down input
+          const int m = lane;
+          uint32_t codes[kTerms], scales;
+          split_block8(lds_act[2 * m], lds_act[2 * m + 16], lds_act[2 * m + 1], lds_act[2 * m + 17],
+                       codes, scales);
+          const size_t blk = (size_t)slot * nbI + pair;
+          uint32_t* dst = reinterpret_cast<uint32_t*>(a.dimg + blk * kImgBytes);
+#pragma unroll
+          for (int t = 0; t < kTerms; ++t) st_sc1(dst + t * 8 + m, codes[t]);
+          if (m == 0) st_sc1(a.dsc + blk, scales);
+          vm_drain();  // image stores complete before the count that announces them
+        }
       }
+      TRACE(4);
     }
+    // counted even when routing failed, so later launches stay in step
+    if (tid == 0) count(a.fs + FS_GU, gid);
   } else {
     // ------------------------------------------------------------- down
-    const int q = bid - a.R - a.NG;
+    const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(a, epoch, sel_i, sel_w)) {
+    if (wave == 0 && !route_wave(a, seq, sel_i, sel_w, lds_route)) {
       if (lane == 0) ok_flag = 0, fail(a);
     }
     __syncthreads();
+    TRACE(1);
     if (ok_flag) {
       const int S = (nbI + 3) >> 2;
       const int row = q * 16 + i;
       const uint64_t rb = (uint64_t)nbI * 17;
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
-      // prefetch this wave's first slot's down weights (independent of gate/up)
-      uint32_t ad[kDnSteps][4], sd[kDnSteps];
+      RawBlk rd[kSteps];
       int slot = wave;
-      if (slot < a.k) load_down_rows(a.down + a.down_off[sel_i[slot]] + (uint64_t)row * rb, S, nbI, g, ad, sd);
-      // wait for every gate/up workgroup of this launch
-      if (tid == 0) {
-        uint32_t it = 0;
-        while (ld_sc1(a.sync + SW_GU_DONE) < (uint32_t)a.NG) {
-          if (++it > a.spin_limit) {
-            ok_flag = 0, fail(a);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-      }
+      const uint8_t* D = a.down + a.down_off[sel_i[slot < a.k ? slot : 0]] + (uint64_t)row * rb;
+      if (slot < a.k) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
+      // this thread's output-row bias terms, also independent of gate/up
+      float ybias = 0.f;
+      if (tid < 16 && a.down_b)
+        for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
+      TRACE(2);
+      if (wave == 0 && !wait_count(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+        ok_flag = 0, fail(a);
       __syncthreads();
+      TRACE(3);
       if (ok_flag) {
-        // all k down B images -> LDS
-        const int n8 = a.k * nbI * kImgBytes / 8;
-        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.dimg);
-        unsigned long long* dst = reinterpret_cast<unsigned long long*>(lds_img);
-        for (int j = tid; j < n8; j += 256) dst[j] = ld_sc1(src + j);
-        for (int j = tid; j < a.k * nbI; j += 256) lds_sc[j] = ld_sc1(a.dsc + j);
-        __syncthreads();
-        for (; slot < a.k; slot += 4) {
-          if (slot != wave) load_down_rows(a.down + a.down_off[sel_i[slot]] + (uint64_t)row * rb, S, nbI, g, ad, sd);
-          const uint8_t* img = lds_img + (size_t)slot * nbI * kImgBytes;
-          const uint32_t* sc = lds_sc + slot * nbI;
+        uint8_t* wimg = lds_img + (size_t)wave * kImgVec * 1024;  // this wave's slot image
+        uint32_t* wsc = lds_sc + wave * 128;
+        if (slot < a.k) {  // one slot per wave (top_k <= 4)
+          {  // slot image -> LDS with direct global->LDS loads (no VGPRs in flight)
+            const uint8_t* src = a.dimg + (size_t)slot * nbI * kImgBytes;
+            const int n16 = nbI * kImgBytes / 16;
 #pragma unroll
-          for (int j = 0; j < kDnSteps; ++j) {
-            if (j < S) {
-              i32x8 B;
-              int sb;
-              load_b(img, sc, j, nbI, i, g, B, sb);
-              d = mfma_fp4(ad[j], sd[j], B, sb, d);
+            for (int j = 0; j < kImgVec; ++j) {
+              if (64 * j < n16) {
+                const int idx = min(lane + 64 * j, n16 - 1);
+                __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, wimg + 1024 * j, 16, 0, 16 /* sc1 */);
+              }
             }
+            const uint32_t sc0 = ld_sc1(a.dsc + slot * nbI + min(lane, nbI - 1));
+            const uint32_t sc1v = ld_sc1(a.dsc + slot * nbI + min(lane + 64, nbI - 1));
+            if (lane < nbI) wsc[lane] = sc0;
+            if (lane + 64 < nbI) wsc[lane + 64] = sc1v;
+            vm_drain();
+            __builtin_amdgcn_wave_barrier();
           }
+          TRACE(4);
+          const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
+          d = mfma_chain(rd, sh, S, nbI, wimg, wsc, lds_zero, i, g, d);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -537,10 +530,7 @@ __global__ __launch_bounds__(256) void k_fused_mxfp4(FusedArgs a) {
         __syncthreads();
         if (tid < 16) {
           const int rr = q * 16 + tid;
-          float yv = ((lds_part[tid] + lds_part[16 + tid]) + lds_part[32 + tid]) + lds_part[48 + tid];
-          if (a.down_b)
-            for (int s = 0; s < a.k; ++s)
-              yv = yv + sel_w[s] * a.down_b[(size_t)sel_i[s] * a.H + rr];
+          const float yv = (((lds_part[tid] + lds_part[16 + tid]) + lds_part[32 + tid]) + lds_part[48 + tid]) + ybias;
           if (rr < a.H) a.y[rr] = yv;
         }
       }
@@ -548,59 +538,63 @@ __global__ __launch_bounds__(256) void k_fused_mxfp4(FusedArgs a) {
   }
   // ----------------------------------------------------------------- exit
   __syncthreads();
-  if (tid == 0) {
+  TRACE(5);
+#ifdef MR_FUSED_TRACE
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 8 + 7] = __smid();
+#endif
+  if (tid == 0 && bid >= a.R && bid < a.R + a.ND) {
     vm_drain();
-    const uint32_t total = (uint32_t)(a.R + a.NG + a.ND);
-    if (add_sc1(a.sync + SW_WG_DONE, 1u) == total - 1u) {
-      st_sc1(a.sync + SW_GU_DONE, 0u);
-      st_sc1(a.sync + SW_WG_DONE, 0u);
-      st_sc1(a.sync + SW_EPOCH, epoch + 1u);
-    }
+    const uint32_t done = add_sc1(a.fs + FS_DN, 1u) + 1u;
+    if (done == (seq + 1u) * (uint32_t)a.ND) st_sc1(a.fs + FS_SEQ, seq + 1u);
   }
 }
 
 // Shapes the fused kernel runs; others take the VALU path.
-bool fused_supported(const mr_layer& L) {
-  if (L.type != MR_GGML_MXFP4 || L.d.sh_gate) return false;
-  const int nbH = L.H / 32, nbI = L.I / 32;
-  if ((nbH + 3) / 4 > 2 * kGuSteps) return false;
-  if ((nbI + 3) / 4 > kDnSteps) return false;
-  if ((size_t)L.d.top_k * nbI * (kImgBytes + 4) > 64 * 1024) return false;
-  if ((size_t)nbH * kImgBytes / 8 > (size_t)256 * kImgRegs) return false;
-  if (L.I % 32 != 0 || L.H % 16 != 0) return false;
+uint64_t fused_layer_sync_bytes() { return (uint64_t)kLayerSyncWords * 4; }
+
+bool fused_supported(const mr_layer& L, int n_cu) {
+  if (L.type != MR_GGML_MXFP4 || L.d.sh_gate || L.d.top_k > 4) return false;
+  const uint64_t R = (L.E + 3) / 4, ND = (L.H + 15) / 16, NG = (uint64_t)L.d.top_k * (L.I / 32);
+  if (R + ND >= (uint64_t)n_cu || R + ND + NG > 3ull * n_cu) return false;  // one dispatch round
+  const uint64_t nbH = L.H / 32, nbI = L.I / 32;
+  if ((nbH + 3) / 4 > (uint64_t)kSteps || (nbI + 3) / 4 > (uint64_t)kSteps) return false;
+  if (nbH > 96 || nbI * kImgBytes > (uint64_t)kImgVec * 64 * 16 || nbI > 128) return false;
+  if (L.E > 512 || L.H % 32 != 0 || L.I % 32 != 0) return false;
   return true;
 }
 
-uint64_t fused_scratch_bytes(uint64_t H, uint64_t I, uint64_t k) {
-  return (H / 32) * (kImgBytes + 4) + k * (I / 32) * (kImgBytes + 4) + 1024;
-}
+#ifdef MR_FUSED_TRACE
+unsigned long long* g_fused_trace = nullptr;
+extern "C" void mr_debug_fused_trace(void* dev_buf) { g_fused_trace = (unsigned long long*)dev_buf; }
+#endif
 
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* sync, uint8_t* img_base, uint32_t spin_limit) {
+                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu) {
   FusedArgs a{};
+#ifdef MR_FUSED_TRACE
+  a.trace = g_fused_trace;
+#endif
   a.gate = L.d.gate->base, a.up = L.d.up->base, a.down = L.d.down->base;
   a.gate_off = L.d.gate->d_offsets, a.up_off = L.d.up->d_offsets, a.down_off = L.d.down->d_offsets;
   a.gate_b = L.d.gate_bias, a.up_b = L.d.up_bias, a.down_b = L.d.down_bias;
   a.router_w = L.d.router_w, a.router_b = L.d.router_b, a.mask = L.d.dummy_mask;
-  a.x = x, a.y = y, a.sync = sync;
-  const uint64_t nbH = L.H / 32, nbI = L.I / 32;
-  uint8_t* p = img_base;
-  a.ximg = p, p += nbH * kImgBytes;
-  a.xsc = reinterpret_cast<uint32_t*>(p), p += ((nbH * 4 + 255) / 256) * 256;
-  a.dimg = p, p += (uint64_t)L.d.top_k * nbI * kImgBytes;
-  a.dsc = reinterpret_cast<uint32_t*>(p);
-  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)L.d.top_k;
+  a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
+  const uint64_t nbH = L.H / 32, nbI = L.I / 32, k = L.d.top_k;
+  a.dimg = img_base;
+  a.dsc = reinterpret_cast<uint32_t*>(img_base + k * nbI * kImgBytes);
+  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k;
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   a.R = (int)((L.E + 3) / 4);
-  a.NG = (int)(L.d.top_k * (L.I / 32));
+  a.NG = (int)(k * nbI);
   a.ND = (int)((L.H + 15) / 16);
   a.spin_limit = spin_limit;
-  const uint64_t img = std::max<uint64_t>(nbH, (uint64_t)L.d.top_k * nbI) * kImgBytes;
-  const uint64_t nsc = std::max<uint64_t>(nbH, (uint64_t)L.d.top_k * nbI);
-  a.lds_img_bytes = (uint32_t)img;
-  const size_t lds = img + nsc * 4;
+  // gate/up: x image (nbH blocks); down: one padded slot image per wave
+  const uint64_t img_bytes = std::max<uint64_t>(nbH * kImgBytes, 4ull * kImgVec * 1024);
+  const uint64_t sc_words = std::max<uint64_t>(nbH, 4ull * 128);
+  a.lds_img_bytes = (uint32_t)img_bytes;
+  const size_t lds = img_bytes + sc_words * 4;
   ProfScope ps(K, "fused_layer");
-  hipLaunchKernelGGL(k_fused_mxfp4, dim3(a.R + a.NG + a.ND), dim3(256), lds, K.s, a);
+  hipLaunchKernelGGL(k_fused_mxfp4, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
   return hipGetLastError();
 }
 

@@ -110,6 +110,7 @@ struct mr_layer {
   mr_layer_desc d{};
   uint32_t H = 0, I = 0, E = 0, Ish = 0;
   int type = 0;
+  uint32_t* fused_sync = nullptr;  // device sync block of the fused decode kernel
 };
 
 struct mr_graph {
@@ -133,8 +134,9 @@ hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks,
 
 // Fused single-launch MXFP4 decode layer (mr_fused.hip).
 constexpr int kSyncErrWord = 96;  // uint32 index of the fused kernel's error word
-bool fused_supported(const mr_layer& L);
+bool fused_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* sync, uint8_t* img_base, uint32_t spin_limit);
+                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu);
+uint64_t fused_layer_sync_bytes();
 
 }  // namespace mr

@@ -25,35 +25,42 @@ HIP_FLAGS = [
 ]
 
 
+EXTRA_FLAGS = os.environ.get("MOE_ROCM_EXTRA_FLAGS", "").split()
+
+
 def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *EXTRA_FLAGS, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
-        cmd = [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *HIP_FLAGS, *EXTRA_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    OBJ_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, out: Path | None = None, obj_dir: Path | None = None) -> Path:
+    global OBJ_DIR
+    if obj_dir is not None:
+        OBJ_DIR = obj_dir
+    lib_path = out or LIB_PATH
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {lib_path}")
+    return lib_path
 
 
 if __name__ == "__main__":
