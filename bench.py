@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=16)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain copy kernel of known size (counter calibration under rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -71,8 +73,36 @@ def cpu_baseline(layers, specs, n_layers_sample: int, n_tokens_sample: int, thre
     return n_lt / t_total  # layer-tokens per second
 
 
+def copy_calibration(n_bytes: int = 1 << 30, reps: int = 4) -> None:
+    """A plain streaming kernel of known traffic: reads n_bytes, writes n_bytes
+    per dispatch (torch elementwise multiply on float32). Under rocprofv3 --pmc,
+    FETCH_SIZE / WRITE_SIZE of this kernel over n_bytes is the counter's scale."""
+    import torch
+
+    a = torch.ones(n_bytes // 4, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        torch.mul(a, 2.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"read_bytes": n_bytes, "write_bytes": n_bytes,
+                                           "dispatches": reps, "kernel": "torch mul float32"}}))
+
+
+def measured_traffic(config: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration), or None when no summary exists for this workload."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    return json.loads(f.read_text()).get(f"C{config}")
+
+
 def main():
     a = parse()
+    if a.copy_calibration:
+        copy_calibration()
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the MoE path is measured on "
                           "one MI355X; multi-GPU expert parallelism is a design note, not a run",
@@ -156,7 +186,12 @@ def main():
     ctx.set_option(M.OPT_PROFILE, 0)
     dom = max(kern, key=lambda k: kern[k][1])
     n_dom, tot_dom = kern[dom]
-    avg_ms = tot_dom / n_dom
+    if set(kern) == {dom}:
+        # one kernel per layer: its average launch is the timed region's event
+        # time over the launches in it (no per-launch event overhead)
+        avg_ms, avg_how = ms / (K * n_layers), "timed-region events / launches"
+    else:
+        avg_ms, avg_how = tot_dom / n_dom, "per-launch events (eager profile pass)"
     s0 = specs[0]
     t = s0.ggml_type
     mb = lambda r, c: M.synth.matrix_bytes(t, r, c)  # noqa: E731
@@ -170,6 +205,9 @@ def main():
         per_launch = s0.n_experts * s0.hidden * 4
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     log("kernels: " + ", ".join(f"{k}: n={v[0]} avg={v[1] / v[0] * 1e3:.2f}us" for k, v in kern.items()))
+
+    tr = measured_traffic(a.config)
+    traffic = None if tr is None or tr.get("kernel") != dom else int(tr["bytes_per_launch"])
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -206,8 +244,9 @@ def main():
         "tflops": round(tok_s * flops_per_token / 1e12, 3),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": int(per_launch),
-                     "avg_launch_us": round(avg_ms * 1e3, 3)},
+                     "traffic": traffic, "bytes_per_launch": int(per_launch),
+                     "avg_launch_us": round(avg_ms * 1e3, 3), "avg_launch_method": avg_how,
+                     "traffic_source": None if traffic is None else "profiles/traffic.json (rocprofv3 --pmc)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
