@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=256, help="timed decode tokens")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--kernel", default="auto", choices=["auto", "valu", "mfma"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "valu", "fused"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=16)
@@ -113,7 +113,7 @@ def main():
 
     ctx = M.Context(0)
     if a.kernel != "auto":
-        ctx.set_option(M.OPT_DECODE_KERNEL, {"valu": M.DECODE_VALU, "mfma": M.DECODE_MFMA}[a.kernel])
+        ctx.set_option(M.OPT_DECODE_KERNEL, {"valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel])
     specs = W.config_layers(a.config)
     if a.config == 5:
         log("config 5 is the batched path; use tests/bench_batched via --config 5 in a later build")

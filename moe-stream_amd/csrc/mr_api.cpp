@@ -276,7 +276,7 @@ void* mr_ctx_stream(const mr_ctx* c) { return c ? static_cast<void*>(c->stream) 
 int mr_ctx_set_option(mr_ctx* c, int option, int value) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   if (option == MR_OPT_DECODE_KERNEL) {
-    if (value < MR_DECODE_AUTO || value > MR_DECODE_MFMA)
+    if (value < MR_DECODE_AUTO || value > MR_DECODE_FUSED)
       return set_err(c, MR_E_INVAL, "decode kernel %d unknown", value);
     c->decode_kernel = value;
     return MR_OK;
@@ -509,7 +509,7 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   L->ctx = c;
   L->d = *d;
   L->H = H, L->I = I, L->E = E, L->Ish = Ish, L->type = type;
-  if (has_dev(c) && mr::fused_supported(*L, c->n_cu)) {
+  if (has_dev(c) && (mr::fused_supported(*L, c->n_cu) || mr::fused_q4k_supported(*L, c->n_cu))) {
     // sync block of the fused decode kernel: counters start at zero
     int rc = bind(c);
     void* fs = nullptr;
@@ -601,13 +601,22 @@ int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
     return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
   mr::Scratch& s = c->scratch;
   hipError_t e;
-  if (c->decode_kernel != MR_DECODE_VALU && L->fused_sync && mr::fused_supported(*L, c->n_cu)) {
-    c->fused_used = true;
-    e = mr::launch_fused(c->launch(), *L, x, y, s.sync + mr::kSyncErrWord, static_cast<uint8_t*>(s.mfma_b), c->spin_limit, c->n_cu);
-    return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
+  if (c->decode_kernel != MR_DECODE_VALU && L->fused_sync) {
+    uint32_t* err = s.sync + mr::kSyncErrWord;
+    uint8_t* img = static_cast<uint8_t*>(s.mfma_b);
+    if (mr::fused_supported(*L, c->n_cu)) {
+      c->fused_used = true;
+      e = mr::launch_fused(c->launch(), *L, x, y, err, img, c->spin_limit, c->n_cu);
+      return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
+    }
+    if (mr::fused_q4k_supported(*L, c->n_cu)) {
+      c->fused_used = true;
+      e = mr::launch_fused_q4k(c->launch(), *L, x, y, err, img);
+      return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
+    }
   }
-  if (c->decode_kernel == MR_DECODE_MFMA)
-    return set_err(c, MR_E_UNSUPPORTED, "the fused MFMA decode kernel does not cover this layer shape");
+  if (c->decode_kernel == MR_DECODE_FUSED)
+    return set_err(c, MR_E_UNSUPPORTED, "the fused decode kernels do not cover this layer shape");
   e = mr::launch_router_logits(c->launch(), *L, x, 1, s.logits);
   if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
   if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, 1, s.idx, s.w, s.act, s.act_sh, y);

@@ -42,6 +42,7 @@
 // counters for the next launch.
 #include "mr_device.h"
 #include "mr_internal.h"
+#include "mr_fused_common.h"
 
 #include <algorithm>
 
@@ -53,23 +54,6 @@ constexpr int kRouterVec = 12;          // float4 pairs per lane of a router row
 constexpr int kImgVec = 12;             // 16-byte image loads per lane for one slot: I <= 3072
 constexpr int kImgBytes = kTerms * 32;  // B image bytes per 32-element block
 
-// Per-layer sync block (uint32 words, zeroed once at layer creation). The
-// counters only grow: launch n of a layer waits for (n+1)*E logits and
-// (n+1)*NG gate/up units, so nothing has to be reset between launches. The
-// producer counters are spread over kCopies lines (copy = producer id % kCopies)
-// and incremented without waiting for a return value; a waiter sums the copies.
-constexpr int kCopies = 8;
-enum : int {
-  FS_SEQ = 0,       // launches completed (advanced by the last down workgroup)
-  FS_DN = 32,       // down workgroups finished (returning atomic)
-  FS_ROUTE = 256,   // [kCopies] x 64 words: logits published
-  FS_GU = 768,      // [kCopies] x 64 words: gate/up units finished
-  FS_LOGITS = 1280  // [E] logits of the current launch
-};
-constexpr int kLayerSyncWords = FS_LOGITS + 512;
-constexpr int kRouteLdsOff = 32768;  // byte offset of the routing scratch in dynamic LDS
-static_assert(96 * kImgBytes <= kRouteLdsOff && kRouteLdsOff + 512 * 4 <= 4 * kImgVec * 1024,
-              "routing scratch must clear the x image and fit in the slot images");
 
 struct FusedArgs {
   const uint8_t* gate;
@@ -97,76 +81,8 @@ struct FusedArgs {
   int R, NG, ND;
   uint32_t spin_limit;
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
-  unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][8] timestamps
+  unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][16] timestamps
 };
-
-#ifdef MR_FUSED_TRACE
-#define TRACE(slot)                                                                       \
-  do {                                                                                    \
-    if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 8 + (slot)] = wall_clock64(); \
-  } while (0)
-#else
-#define TRACE(slot) \
-  do {              \
-  } while (0)
-#endif
-
-// ---- DPP ---------------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1;      // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4E;      // quad_perm [2,3,0,1]
-constexpr int kDppHMirror = 0x141;  // row_half_mirror: lane i <-> 7-i within 8
-
-// max over each aligned group of 8 lanes, in every lane of the group
-__device__ __forceinline__ float max8(float v) {
-  v = fmaxf(v, dpp_f<kDppXor1>(v));
-  v = fmaxf(v, dpp_f<kDppXor2>(v));
-  return fmaxf(v, dpp_f<kDppHMirror>(v));
-}
-// sum over each quad, in every lane of the quad
-__device__ __forceinline__ float sum4(float v) {
-  v += dpp_f<kDppXor1>(v);
-  return v + dpp_f<kDppXor2>(v);
-}
-
-// ---- agent-coherent accesses (global_load/store ... sc1) ---------------------------
-__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_sc1(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t add_sc1(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// All vector memory operations this wave has issued have completed.
-__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Count one finished producer (no return value is waited for).
-__device__ __forceinline__ void count(uint32_t* copies, int id) {
-  (void)__hip_atomic_fetch_add(copies + 64 * (id % kCopies), 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-}
-// Bounded wait (one wave) until the counter copies sum to at least `target`
-// (wrap-around safe); false if the limit ran out.
-__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
-  const int lane = threadIdx.x & 63;
-  for (uint32_t it = 0;; ++it) {
-    uint32_t c = lane < kCopies ? ld_sc1(copies + 64 * lane) : 0u;
-    // sum of kCopies (= 8) lanes: exact in uint32 via two 16-bit halves in floats
-    float lo = (float)(c & 0xFFFFu), hi = (float)(c >> 16);
-    lo += dpp_f<kDppXor1>(lo), hi += dpp_f<kDppXor1>(hi);
-    lo += dpp_f<kDppXor2>(lo), hi += dpp_f<kDppXor2>(hi);
-    lo += dpp_f<kDppHMirror>(lo), hi += dpp_f<kDppHMirror>(hi);
-    const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)lo + ((uint32_t)hi << 16)));
-    if ((int32_t)(sum - target) >= 0) return true;
-    if (it >= limit) return false;
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
 
 // ---- e4m3 activation split -----------------------------------------------------------
 // One 32-element block is held by 8 lanes; lane m holds MFMA positions
@@ -263,57 +179,6 @@ __device__ __forceinline__ f32x4 mfma_chain(const RawBlk (&rw)[kSteps], uint32_t
   return acc;
 }
 
-// ---- routing ----------------------------------------------------------------------------
-// Wave 0 of a consumer workgroup: wait until every logit of this launch is
-// published, then select the top-k (largest first, ties to the lower index;
-// top_k_routing layer.rs:2346-2403) by ranking each expert against all others
-// in LDS, and write slot -> (expert, weight) to LDS.
-__device__ bool route_wave(const FusedArgs& a, uint32_t seq, int* sel_i, float* sel_w,
-                           float* lds_v) {
-  const int lane = threadIdx.x & 63;
-  if (!wait_count(a.fs + FS_ROUTE, (seq + 1u) * (uint32_t)a.E, a.spin_limit)) return false;
-  for (int e = lane; e < a.E; e += 64) lds_v[e] = __uint_as_float(ld_sc1(a.fs + FS_LOGITS + e));
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  const bool softmax_after = (a.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
-  if (!softmax_after) {  // rank by probability: softmax over all experts first
-    float m = -INFINITY;
-    for (int e = lane; e < a.E; e += 64) m = fmaxf(m, lds_v[e]);
-    m = wave_max(m);
-    float s = 0.f;
-    for (int e = lane; e < a.E; e += 64) s += __expf(lds_v[e] - m);
-    s = wave_sum(s);
-    for (int e = lane; e < a.E; e += 64) lds_v[e] = __expf(lds_v[e] - m) / s;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  }
-  if (lane < a.k) sel_i[lane] = 0, sel_w[lane] = 0.f;  // in range even if a NaN breaks the ranks
-  for (int e = lane; e < a.E; e += 64) {
-    const float v = lds_v[e];
-    int r = 0;
-    for (int e2 = 0; e2 < a.E; ++e2) {
-      const float v2 = lds_v[e2];
-      r += (v2 > v || (v2 == v && e2 < e)) ? 1 : 0;
-    }
-    if (r < a.k) sel_i[r] = e, sel_w[r] = v;
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-  if (lane == 0) {  // weights over the k selected values, in selection order
-    if (softmax_after) {
-      float m = -INFINITY, s = 0.f;
-      for (int r = 0; r < a.k; ++r) m = fmaxf(m, sel_w[r]);
-      for (int r = 0; r < a.k; ++r) s = s + __expf(sel_w[r] - m);
-      for (int r = 0; r < a.k; ++r) sel_w[r] = __expf(sel_w[r] - m) / s;
-    } else if (a.flags & MR_ROUTE_NORM_TOPK) {
-      float s = 0.f;
-      for (int r = 0; r < a.k; ++r) s = s + sel_w[r];
-      for (int r = 0; r < a.k; ++r) sel_w[r] = sel_w[r] / s;
-    }
-  }
-  return true;
-}
-
-__device__ __forceinline__ void fail(const FusedArgs& a) { st_sc1(a.err, 1u); }
-
 // A operands (raw windows) of one 16-row tile, all K steps (S is wave-uniform).
 // Blocks past the row end (last step, lane groups g beyond nb) load the row's
 // last block instead: their B operand is all zero, so they add exactly 0.
@@ -337,18 +202,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   __shared__ float lds_act[32];
   __shared__ int sel_i[16];
   __shared__ float sel_w[16];
+  __shared__ int sel_o[16];
   __shared__ int ok_flag;
   __shared__ __align__(16) uint8_t lds_zero[32];
-  // routing scratch: past the x image of gate/up workgroups (<= 12 KiB) and in
-  // the slot images of down workgroups, which are written only after routing
-  float* lds_route = reinterpret_cast<float*>(lds_img + kRouteLdsOff);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int bid = blockIdx.x;
   const int nbH = a.H >> 5, nbI = a.I >> 5;
   TRACE(0);
-  const uint32_t seq = ld_sc1(a.fs + FS_SEQ);
+  const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
+  const RouteCfg rc{a.fs, (uint32_t)a.E, a.E, a.k, a.flags, a.spin_limit, a.trace};
   if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
 
   if (bid < a.R) {
@@ -377,10 +241,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         if (a.router_b) acc = acc + a.router_b[e];
         if (a.mask) acc = acc + a.mask[e];
         st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
-        vm_drain();  // the logit is visible before the count that announces it
-        count(a.fs + FS_ROUTE, e);
+        vm_drain();  // the logit is stored before the barrier that precedes its count
       }
     }
+    __syncthreads();
+    if (tid == 0) count(a.fs + FS_ROUTE, bid, (uint32_t)min(4, a.E - bid * 4));  // this workgroup's logits
     TRACE(1);
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
@@ -414,8 +279,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     }
     TRACE(1);
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(a, seq, sel_i, sel_w, lds_route)) {
-      if (lane == 0) ok_flag = 0, fail(a);
+    if (wave == 0 && !route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+      if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();  // routing and x image ready
     TRACE(2);
@@ -474,8 +339,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     // ------------------------------------------------------------- down
     const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(a, seq, sel_i, sel_w, lds_route)) {
-      if (lane == 0) ok_flag = 0, fail(a);
+    if (wave == 0 && !route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+      if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();
     TRACE(1);
@@ -493,8 +358,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       TRACE(2);
-      if (wave == 0 && !wait_count(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
-        ok_flag = 0, fail(a);
+      if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+        ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);
       if (ok_flag) {
@@ -530,7 +395,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         __syncthreads();
         if (tid < 16) {
           const int rr = q * 16 + tid;
-          const float yv = (((lds_part[tid] + lds_part[16 + tid]) + lds_part[32 + tid]) + lds_part[48 + tid]) + ybias;
+          float yv = 0.f;  // slots in ascending expert order (layer.rs:1092-1106)
+          for (int p = 0; p < a.k; ++p) yv = yv + lds_part[sel_o[p] * 16 + tid];
+          yv = yv + ybias;
           if (rr < a.H) a.y[rr] = yv;
         }
       }
@@ -540,13 +407,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   __syncthreads();
   TRACE(5);
 #ifdef MR_FUSED_TRACE
-  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 8 + 7] = __smid();
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + 7] = __smid();
 #endif
-  if (tid == 0 && bid >= a.R && bid < a.R + a.ND) {
-    vm_drain();
-    const uint32_t done = add_sc1(a.fs + FS_DN, 1u) + 1u;
-    if (done == (seq + 1u) * (uint32_t)a.ND) st_sc1(a.fs + FS_SEQ, seq + 1u);
-  }
+  if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
 }
 
 // Shapes the fused kernel runs; others take the VALU path.
@@ -556,6 +419,7 @@ bool fused_supported(const mr_layer& L, int n_cu) {
   if (L.type != MR_GGML_MXFP4 || L.d.sh_gate || L.d.top_k > 4) return false;
   const uint64_t R = (L.E + 3) / 4, ND = (L.H + 15) / 16, NG = (uint64_t)L.d.top_k * (L.I / 32);
   if (R + ND >= (uint64_t)n_cu || R + ND + NG > 3ull * n_cu) return false;  // one dispatch round
+  if (R + ND + NG > (uint64_t)kMaxGrid) return false;
   const uint64_t nbH = L.H / 32, nbI = L.I / 32;
   if ((nbH + 3) / 4 > (uint64_t)kSteps || (nbI + 3) / 4 > (uint64_t)kSteps) return false;
   if (nbH > 96 || nbI * kImgBytes > (uint64_t)kImgVec * 64 * 16 || nbI > 128) return false;

@@ -1,0 +1,292 @@
+// mr_fused_common.h -- pieces shared by the single-launch decode kernels
+// (mr_fused.hip: MXFP4 on MFMA; mr_fused_q4k.hip: Q4_K on integer dot products).
+//
+// A fused decode launch splits its grid into roles (router, gate/up, down) that
+// hand results to each other through HBM inside the one launch. Hand-offs use:
+//  * agent-coherent accesses (global_load/store ... sc1: they bypass the
+//    non-coherent per-CU caches and meet in L2), ordered by s_waitcnt;
+//  * monotonic counters in a per-layer sync block: launch n of a layer waits
+//    until a counter reaches (n+1) * producers, so nothing is reset between
+//    launches. Producers increment one of kCopies copies (spread over separate
+//    cache lines) without waiting for a return value; waiters sum the copies.
+//    Each workgroup keeps its own launch number n (no exit atomic);
+//  * bounded waits: a wait that runs out of iterations sets the context error
+//    word (read and cleared by mr_sync) and the launch still exits normally.
+#pragma once
+
+#include "../../include/moe_rocm.h"
+#include "mr_device.h"
+
+namespace mr {
+
+constexpr int kCopies = 64;     // copies of each producer counter, one 128-byte line apart
+constexpr int kCopyStride = 32;  // words
+enum : int {
+  FS_ROUTE = 0,                                // [kCopies] counter: logits published
+  FS_GU = FS_ROUTE + kCopies * kCopyStride,    // [kCopies] counter: gate/up units finished
+  FS_LOGITS = FS_GU + kCopies * kCopyStride,   // logits of the current launch (E experts, then extras)
+  FS_WGSEQ = FS_LOGITS + 1024                  // [grid] launches completed, one word per workgroup
+};
+constexpr int kMaxLogits = 1024;
+constexpr int kMaxGrid = 1024;
+constexpr int kLayerSyncWords = FS_WGSEQ + kMaxGrid;
+
+// Launch sequence number of this layer's kernel. Every launch of a layer runs
+// the same grid, so each workgroup keeps its own count (read at entry, stored
+// +1 at exit): all workgroups of a launch read the same value, with no atomic.
+__device__ __forceinline__ uint32_t* wg_seq_word(uint32_t* fs) { return fs + FS_WGSEQ + blockIdx.x; }
+
+#ifdef MR_FUSED_TRACE
+#define TRACE(slot)                                                                       \
+  do {                                                                                    \
+    if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + (slot)] = wall_clock64(); \
+  } while (0)
+#define RTRACE(slot)                                                                             \
+  do {                                                                                           \
+    if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 16 + 8 + (slot)] = wall_clock64(); \
+  } while (0)
+#else
+#define TRACE(slot) \
+  do {              \
+  } while (0)
+#define RTRACE(slot) \
+  do {               \
+  } while (0)
+#endif
+
+// ---- DPP ---------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppHMirror = 0x141;  // row_half_mirror: lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;   // row_mirror: lane i <-> 15-i within 16
+
+// max over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  return fmaxf(v, dpp_f<kDppHMirror>(v));
+}
+// sum over each quad, in every lane of the quad
+__device__ __forceinline__ float sum4(float v) {
+  v += dpp_f<kDppXor1>(v);
+  return v + dpp_f<kDppXor2>(v);
+}
+// sum over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float sum8(float v) {
+  v = sum4(v);
+  return v + dpp_f<kDppHMirror>(v);
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int L>
+__device__ __forceinline__ uint32_t lane_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, L);
+}
+template <int L>
+__device__ __forceinline__ float lane_f(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), L));
+}
+// Whole-wave reductions (all 64 lanes active), result uniform: DPP inside each
+// row of 16 lanes, then the four row results through readlane.
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+  v += dpp_u<kDppXor1>(v);
+  v += dpp_u<kDppXor2>(v);
+  v += dpp_u<kDppHMirror>(v);
+  v += dpp_u<kDppMirror>(v);
+  return (lane_u<0>(v) + lane_u<16>(v)) + (lane_u<32>(v) + lane_u<48>(v));
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+  v = max(v, dpp_u<kDppXor1>(v));
+  v = max(v, dpp_u<kDppXor2>(v));
+  v = max(v, dpp_u<kDppHMirror>(v));
+  v = max(v, dpp_u<kDppMirror>(v));
+  return max(max(lane_u<0>(v), lane_u<16>(v)), max(lane_u<32>(v), lane_u<48>(v)));
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+  v = min(v, dpp_u<kDppXor1>(v));
+  v = min(v, dpp_u<kDppXor2>(v));
+  v = min(v, dpp_u<kDppHMirror>(v));
+  v = min(v, dpp_u<kDppMirror>(v));
+  return min(min(lane_u<0>(v), lane_u<16>(v)), min(lane_u<32>(v), lane_u<48>(v)));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_f<0>(v), lane_f<16>(v)), fmaxf(lane_f<32>(v), lane_f<48>(v)));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  return (lane_f<0>(v) + lane_f<16>(v)) + (lane_f<32>(v) + lane_f<48>(v));
+}
+
+// ---- agent-coherent accesses (global_load/store ... sc1) ---------------------------
+__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_sc1(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_sc1(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All vector memory operations this wave has issued have completed.
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// All LDS operations this wave has issued have completed.
+__device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Count n finished producer items on copy (id % kCopies) (no return value is waited for).
+__device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u) {
+  (void)__hip_atomic_fetch_add(copies + kCopyStride * (id % kCopies), n, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+// Bounded wait (one full wave) until the counter copies sum to at least `target`
+// (wrap-around safe); false if the limit ran out. SLEEP: s_sleep units (64 clocks)
+// between polls (longer for waits that overlap weight streaming).
+template <int SLEEP = 2>
+__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
+  const int lane = threadIdx.x & 63;
+  for (uint32_t it = 0;; ++it) {
+    const uint32_t sum = wave_sum_u(ld_sc1(copies + kCopyStride * lane));
+    if ((int32_t)(sum - target) >= 0) return true;
+    if (it >= limit) return false;
+    __builtin_amdgcn_s_sleep(SLEEP);
+  }
+}
+
+// ---- routing ----------------------------------------------------------------------------
+struct RouteCfg {
+  const uint32_t* fs;  // layer sync block
+  uint32_t n_logits;   // logits published per launch (E, plus extras)
+  int E, k;
+  uint32_t flags;      // MR_ROUTE_*
+  uint32_t spin_limit;
+  unsigned long long* trace;  // MR_FUSED_TRACE builds only
+};
+
+// Order-preserving key of a float: larger float <=> larger unsigned key.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+constexpr int kRouteVals = 8;  // experts per lane in routing: E <= 512
+
+// (key desc, expert asc) compare-exchange of list entries a < b
+__device__ __forceinline__ void cas_desc(uint32_t& ka, int& ia, uint32_t& kb, int& ib) {
+  const bool sw = kb > ka || (kb == ka && ib < ia);
+  const uint32_t tk = sw ? kb : ka;
+  const int ti = sw ? ib : ia;
+  kb = sw ? ka : kb, ib = sw ? ia : ib;
+  ka = tk, ia = ti;
+}
+
+// Wave 0 of a consumer workgroup (all 64 lanes): wait until every logit of this
+// launch is published, then select the top-k (largest first, ties to the lower
+// index; top_k_routing layer.rs:2346-2403). Expert e = lane + 64*j is value j of
+// a lane; each lane sorts its values (Batcher network), then k rounds take the
+// wave-wide largest head (DPP max; ties: the lowest expert index) and pop it.
+// Writes slot -> (expert, weight) and ord[p] = the slot holding the p-th
+// smallest expert index (the combine order of layer.rs:1092-1106).
+__device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, float* sel_w, int* ord) {
+  const int lane = threadIdx.x & 63;
+  RTRACE(0);
+  if (!wait_count(rc.fs + FS_ROUTE, (seq + 1u) * rc.n_logits, rc.spin_limit)) return false;
+  RTRACE(1);
+  const int nj = (rc.E + 63) >> 6;  // values per lane (wave-uniform)
+  float v[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = (j < nj && e < rc.E) ? __uint_as_float(ld_sc1(rc.fs + FS_LOGITS + e)) : -INFINITY;
+  }
+  const bool softmax_after = (rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
+  if (!softmax_after) {  // rank by probability: softmax over all experts first
+    RTRACE(2);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j) m = fmaxf(m, v[j]);
+    m = wave_max_f(m);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j)
+      if (lane + 64 * j < rc.E) s += __expf(v[j] - m);
+    s = wave_sum_f(s);
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j)
+      if (lane + 64 * j < rc.E) v[j] = __expf(v[j] - m) / s;
+  }
+  RTRACE(3);
+  uint32_t key[kRouteVals];
+  int idx[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {  // + 0.f: -0.0 and +0.0 compare equal, so share a key
+    key[j] = (lane + 64 * j < rc.E) ? order_key(v[j] + 0.f) : 0u;
+    idx[j] = lane + 64 * j;
+  }
+  if (nj == 2) {
+    cas_desc(key[0], idx[0], key[1], idx[1]);
+  } else if (nj > 2) {  // Batcher odd-even merge sort of 8
+#define MR_CAS(a, b) cas_desc(key[a], idx[a], key[b], idx[b])
+    MR_CAS(0, 1), MR_CAS(2, 3), MR_CAS(4, 5), MR_CAS(6, 7);
+    MR_CAS(0, 2), MR_CAS(1, 3), MR_CAS(4, 6), MR_CAS(5, 7);
+    MR_CAS(1, 2), MR_CAS(5, 6);
+    MR_CAS(0, 4), MR_CAS(1, 5), MR_CAS(2, 6), MR_CAS(3, 7);
+    MR_CAS(2, 4), MR_CAS(3, 5);
+    MR_CAS(1, 2), MR_CAS(3, 4), MR_CAS(5, 6);
+#undef MR_CAS
+  }
+  RTRACE(4);
+  uint32_t my_key = 0u;
+  int my_e = 0;
+  for (int r = 0; r < rc.k; ++r) {
+    const uint32_t M = wave_max_u(key[0]);
+    const unsigned long long tied = __ballot(key[0] == M);
+    int wl = __ffsll((long long)tied) - 1;
+    if (__popcll(tied) > 1)  // equal values: the lowest expert index wins
+      wl = (int)(wave_min_u(key[0] == M ? (uint32_t)idx[0] : 0xFFFFFFFFu) & 63u);
+    const int e = min(__builtin_amdgcn_readlane(idx[0], wl), rc.E - 1);
+    if (lane == r) my_key = M, my_e = e;
+    if (lane == wl) {  // pop the head
+#pragma unroll
+      for (int j = 0; j < kRouteVals - 1; ++j) key[j] = key[j + 1], idx[j] = idx[j + 1];
+      key[kRouteVals - 1] = 0u;
+    }
+  }
+  RTRACE(5);
+  // weights over the k selected values (lane r = slot r, in selection order)
+  const bool in = lane < rc.k;
+  float w = in ? key_value(my_key) : 0.f;
+  if (softmax_after) {
+    const float m = lane_f<0>(w);  // slot 0 holds the largest value
+    const float ex = in ? __expf(w - m) : 0.f;
+    w = ex / wave_sum_f(ex);
+  } else if (rc.flags & MR_ROUTE_NORM_TOPK) {
+    w = w / wave_sum_f(w);
+  }
+  int p = 0;  // position of this slot's expert in ascending expert order
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (r < rc.k) p += __builtin_amdgcn_readlane(my_e, r) < my_e ? 1 : 0;
+  if (in) sel_i[lane] = my_e, sel_w[lane] = w, ord[p] = lane;
+  lds_drain();
+  RTRACE(7);
+  return true;
+}
+
+__device__ __forceinline__ void fail(uint32_t* err) { st_sc1(err, 1u); }
+
+}  // namespace mr

@@ -1,0 +1,478 @@
+// mr_fused_q4k.hip -- single-launch Q4_K MoE decode layer for gfx950 (CDNA4).
+//
+// The Q4_K counterpart of k_fused_mxfp4: one kernel per layer and token does
+// the router GEMV (+ the shared-expert gate), top-k routing, gate+up
+// dequant-matvec with SwiGLU/SiLU, down dequant-matvec with the weighted
+// combine in ascending expert order, and the sigmoid-gated shared expert
+// (layer.rs:1012-1027, 1818-1953, 2346-2403; per-expert QMatMul path
+// layer.rs:2099-2147).
+//
+// Weight streaming. A wave owns a region of 8 consecutive rows of one expert
+// matrix; the rows are contiguous in the GGUF layout, so lane l simply loads
+// 16-byte chunks l, l+64, ... of the region (fully coalesced 1 KiB per wave
+// load). A 144-byte super-block is 9 chunks: chunk 0 is the header (d, dmin,
+// 12 scale bytes), chunks 1..8 are the 128 quant bytes. Header chunks are
+// staged in LDS and decoded once per super-block into (d*sc_j, dmin*m_j);
+// quant chunk p (qs bytes 16(p-1)..16p) holds 16 low nibbles = elements
+// 64jj+16hf+t of sub-block 2jj and 16 high nibbles = elements 64jj+32+16hf+t of
+// sub-block 2jj+1 (jj = (p-1)/2, hf = (p-1)%2; dequantize_q4k, dequant.rs:218-262).
+//
+// Dot products. The activation vector is split per 16-element group into two
+// int8 terms: v = s0*t0 + s1*t1 with s0 = max|v|/127, s1 = s0/254, so
+// |v - s0*t0 - s1*t1| <= s0/508 (about 1.6e-5 of the group max). The nibbles
+// (0..15) are already int8 operands after one AND, so a chunk's 32 products
+// are 8 v_dot4_i32_i8 per term, exact in int32. Per sub-block half:
+//   sum_j w_j x_j = (d*sc) * (s0*A0 + s1*A1) - (dmin*m) * sum_j x_j
+// with A0/A1 the integer dot products and sum_j x_j the group sum, the same
+// weights w_j = (d*sc)*q_j - dmin*m the reference dequantizes.
+//
+// Roles (grid order; all workgroups resident, see fused_q4k_supported):
+//   [0, R)       router: one logit per wave (E experts, then x . w_gi of the
+//                shared expert when there is one).
+//   [R, R+ND)    down: 8 output rows; wave w takes slots w, w+4, w+8 (routed
+//                slots, then the shared expert). Down weights are prefetched into
+//                registers before the gate/up results exist.
+//   [R+ND, grid) gate/up: 16 rows of one slot; waves = (gate, up) x 2 halves of
+//                8 rows. Epilogue: bias, activation, x routing weight (sigmoid
+//                gate for the shared expert), int8 split of the 16 results into
+//                the down input image.
+#include "mr_device.h"
+#include "mr_fused_common.h"
+#include "mr_internal.h"
+
+#include <algorithm>
+
+namespace mr {
+
+constexpr int kQ4RouterVec = 12;  // float4 pairs per lane of a router row: H <= 3072
+constexpr int kQ4GuIt = 9;        // chunks per lane of a gate/up region (8 rows x H/256 sb): H <= 2048
+constexpr int kQ4DnIt = 4;        // chunks per lane per slot of a down region (8 rows x I/256 sb): I <= 768
+constexpr int kQ4DnSlots = 3;     // slots per down wave: k + shared <= 12
+constexpr int kQ4MaxH = 2048, kQ4MaxI = 768, kQ4MaxSlots = 4 * kQ4DnSlots;
+constexpr float kInv254 = 1.0f / 254.0f;
+
+// LDS carve-up (bytes), gate/up workgroups
+constexpr int kGuXq = 0;                                 // [H/16][2 x 16 int8] x terms
+constexpr int kGuXs = kGuXq + kQ4MaxH * 2;               // [H/16] float2 (s0, group sum)
+constexpr int kGuHraw = kGuXs + kQ4MaxH / 16 * 8;        // [4 waves][64 sb] raw headers
+constexpr int kGuHdec = kGuHraw + 4 * 64 * 16;           // [4][64 sb][16 floats] decoded
+constexpr int kGuVbuf = kGuHdec + 4 * 64 * 64;           // [4][576] chunk partials
+constexpr int kGuEnd = kGuVbuf + 4 * 576 * 4;
+// down workgroups
+constexpr int kDnGroups = kQ4MaxI / 16;
+constexpr int kDnHq = 0;                                  // [slots][I/16][32] h terms
+constexpr int kDnHs = kDnHq + kQ4MaxSlots * kDnGroups * 32;  // [slots][I/16] float2
+constexpr int kDnHraw = kDnHs + kQ4MaxSlots * kDnGroups * 8 + 1024;  // + 1 KiB load overrun
+constexpr int kDnHdec = kDnHraw + 4 * 24 * 16;
+constexpr int kDnVbuf = kDnHdec + 4 * 24 * 64;
+constexpr int kDnEnd = kDnVbuf + 4 * 216 * 4;
+constexpr int kQ4Smem = kGuEnd > kDnEnd ? kGuEnd : kDnEnd;
+static_assert(72 * (kQ4MaxH / 256) <= 64 * kQ4GuIt && 72 * (kQ4MaxI / 256) <= 64 * kQ4DnIt,
+              "a wave's chunks cover its 8-row region");
+static_assert(72 * (kQ4MaxH / 256) <= 576 && 72 * (kQ4MaxI / 256) <= 216 && 8 * (kQ4MaxI / 256) <= 24,
+              "per-wave LDS slices hold a region's partials and headers");
+
+struct Q4Args {
+  const uint8_t* gate;
+  const uint8_t* up;
+  const uint8_t* down;
+  const uint64_t* gate_off;
+  const uint64_t* up_off;
+  const uint64_t* down_off;
+  const uint8_t* sh_gate;  // shared expert matrices (one expert) or null
+  const uint8_t* sh_up;
+  const uint8_t* sh_down;
+  const float* gate_b;
+  const float* up_b;
+  const float* down_b;
+  const float* router_w;
+  const float* router_b;
+  const float* mask;
+  const float* sh_gate_inp;
+  const float* x;
+  float* y;
+  uint32_t* fs;     // this layer's sync block
+  uint32_t* err;    // context error word
+  uint32_t* himg;   // [ktot][I/16][8 words] int8 terms of the down input
+  float* hsc;       // [ktot][I/16][2] (s0, group sum)
+  int H, I, E, k, ktot, has_sh;
+  uint32_t flags;
+  int act;
+  float alpha, limit;
+  int R, ND, NG;
+  uint32_t spin_limit;
+  unsigned long long* trace;
+};
+
+// ---- int8 two-term split ------------------------------------------------------------------
+// s0 = m/127 (m = max|v| of the group), s1 = s0/254; t0 = rn(v/s0), t1 = rn((v - s0*t0)/s1).
+__device__ __forceinline__ void split_i8(float v, float m, int& t0, int& t1, float& s0) {
+  if (!(m > 0.f)) {
+    t0 = t1 = 0, s0 = 0.f;
+    return;
+  }
+  s0 = m / 127.f;
+  const float s1 = s0 * kInv254;
+  t0 = (int)fminf(fmaxf(rintf(v / s0), -127.f), 127.f);
+  const float r = fmaf(-(float)t0, s0, v);
+  t1 = (int)fminf(fmaxf(rintf(r / s1), -127.f), 127.f);
+}
+
+// ---- one region: 8 rows of a Q4_K matrix --------------------------------------------------
+// ch: the lane's chunks (chunk c = 64*i + lane of the region). nsb: super-blocks per
+// row; nch = 72*nsb. Activation image: terms `xq` ([G][32 B]) and `xs` ([G] (s0, sum)).
+// Leaves each row's dot product in lanes 8*row (row = 0..7).
+template <int IT>
+__device__ __forceinline__ float region_dot(const uint4 (&ch)[IT], int nsb, const uint8_t* xq,
+                                            const float2* xs, uint4* hraw, float* hdec, float* vbuf) {
+  const int lane = threadIdx.x & 63;
+  const int nch = 72 * nsb;
+  // stage the header chunks, then decode super-block `lane`
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = 64 * i + lane;
+    if (c < nch && c % 9 == 0) hraw[c / 9] = ch[i];
+  }
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+  if (lane < 8 * nsb) {
+    const uint4 h = hraw[lane];
+    const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+    const uint32_t s3[3] = {h.y, h.z, h.w};
+    float4* out = reinterpret_cast<float4*>(hdec + lane * 16);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      uint32_t sc0, m0, sc1, m1;
+      q4k_scale_min((uint32_t)j, s3, sc0, m0);
+      q4k_scale_min((uint32_t)j + 1u, s3, sc1, m1);
+      out[j / 2] = float4{__fmul_rn(d, (float)sc0), __fmul_rn(dmin, (float)m0),
+                          __fmul_rn(d, (float)sc1), __fmul_rn(dmin, (float)m1)};
+    }
+  }
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = 64 * i + lane;
+    if (c < nch) {
+      const int sbw = c / 9, p = c - 9 * sbw;
+      float v = 0.f;
+      if (p != 0) {
+        const int row = sbw / nsb, col = sbw - row * nsb;
+        (void)row;
+        const int pp = p - 1, jj = pp >> 1, hf = pp & 1;
+        const int G = col * 16 + jj * 4 + hf;  // low nibbles; high nibbles: G + 2
+        const uint4 l0 = *reinterpret_cast<const uint4*>(xq + G * 32);
+        const uint4 l1 = *reinterpret_cast<const uint4*>(xq + G * 32 + 16);
+        const uint4 h0 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32);
+        const uint4 h1 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32 + 16);
+        const uint32_t w[4] = {ch[i].x, ch[i].y, ch[i].z, ch[i].w};
+        const uint32_t xl0[4] = {l0.x, l0.y, l0.z, l0.w}, xl1[4] = {l1.x, l1.y, l1.z, l1.w};
+        const uint32_t xh0[4] = {h0.x, h0.y, h0.z, h0.w}, xh1[4] = {h1.x, h1.y, h1.z, h1.w};
+        int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int lo = (int)(w[d] & 0x0F0F0F0Fu), hi = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
+          a0 = __builtin_amdgcn_sdot4(lo, (int)xl0[d], a0, false);
+          a1 = __builtin_amdgcn_sdot4(lo, (int)xl1[d], a1, false);
+          b0 = __builtin_amdgcn_sdot4(hi, (int)xh0[d], b0, false);
+          b1 = __builtin_amdgcn_sdot4(hi, (int)xh1[d], b1, false);
+        }
+        const float2 gl = xs[G], gh = xs[G + 2];
+        const float4 dm = *reinterpret_cast<const float4*>(hdec + sbw * 16 + 4 * jj);
+        const float xlo = gl.x * (float)a0 + (gl.x * kInv254) * (float)a1;
+        const float xhi = gh.x * (float)b0 + (gh.x * kInv254) * (float)b1;
+        v = ((dm.x * xlo - dm.y * gl.y) + dm.z * xhi) - dm.w * gh.y;
+      }
+      vbuf[c] = v;
+    }
+  }
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+  // row sums: 8 lanes per row, each over every 8th chunk of the row, then DPP
+  const int row = lane >> 3, j8 = lane & 7, per = 9 * nsb;
+  float s = 0.f;
+  for (int c = j8; c < per; c += 8) s += vbuf[row * per + c];
+  return sum8(s);
+}
+
+// Loads of one region (8 rows x nsb super-blocks at `base`); chunks past the end
+// load the last chunk (ignored).
+template <int IT>
+__device__ __forceinline__ void region_load(const uint8_t* base, int nsb, uint4 (&ch)[IT]) {
+  const int lane = threadIdx.x & 63, nch = 72 * nsb;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = min(64 * i + lane, nch - 1);
+    ch[i] = *reinterpret_cast<const uint4*>(base + (size_t)c * 16);
+  }
+}
+
+__global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
+  __shared__ __align__(16) uint8_t smem[kQ4Smem];
+  __shared__ int sel_i[16];
+  __shared__ float sel_w[17];  // [k]: weight of the shared expert
+  __shared__ int sel_o[16];
+  __shared__ int ok_flag;
+  __shared__ float gu_part[2][16];
+  __shared__ __align__(16) int8_t hb[32];
+  __shared__ float dn_part[kQ4MaxSlots][8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bid = blockIdx.x;
+  const int nsbH = a.H >> 8, nsbI = a.I >> 8, nGI = a.I >> 4;
+  TRACE(0);
+  const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
+  const RouteCfg rc{a.fs, (uint32_t)(a.E + a.has_sh), a.E, a.k, a.flags, a.spin_limit, a.trace};
+
+  if (bid < a.R) {
+    // ------------------------------------------------------------- router
+    const int e = bid * 4 + wave;
+    if (e < a.E + a.has_sh) {
+      const float* w = e < a.E ? a.router_w + (size_t)e * a.H : a.sh_gate_inp;
+      f32x4 xv[kQ4RouterVec], wv[kQ4RouterVec];
+#pragma unroll
+      for (int j = 0; j < kQ4RouterVec; ++j) {
+        const int c = (lane + 64 * j) * 4;
+        const bool in = c < a.H && w != nullptr;
+        xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kQ4RouterVec; ++j) {
+        acc = __builtin_fmaf(xv[j].x, wv[j].x, acc);
+        acc = __builtin_fmaf(xv[j].y, wv[j].y, acc);
+        acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
+        acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) {
+        if (e < a.E) {
+          if (a.router_b) acc = acc + a.router_b[e];
+          if (a.mask) acc = acc + a.mask[e];
+        }
+        st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
+        vm_drain();  // the logit is stored before the barrier that precedes its count
+      }
+    }
+    __syncthreads();
+    if (tid == 0) count(a.fs + FS_ROUTE, bid, (uint32_t)min(4, a.E + a.has_sh - bid * 4));  // this workgroup's logits
+    TRACE(1);
+  } else if (bid >= a.R + a.ND) {
+    // ------------------------------------------------------------- gate/up
+    const int gid = bid - a.R - a.ND;
+    uint8_t* xq = smem + kGuXq;
+    float2* xs = reinterpret_cast<float2*>(smem + kGuXs);
+    // x image: one 16-element group per thread
+    for (int G = tid; G < (a.H >> 4); G += 256) {
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(a.x + G * 16 + 4 * q);
+        v[4 * q] = t.x, v[4 * q + 1] = t.y, v[4 * q + 2] = t.z, v[4 * q + 3] = t.w;
+      }
+      float m = 0.f, sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(v[q])), sum = sum + v[q];
+      uint32_t p0[4] = {0u, 0u, 0u, 0u}, p1[4] = {0u, 0u, 0u, 0u};
+      float s0 = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        int t0, t1;
+        split_i8(v[q], m, t0, t1, s0);
+        p0[q >> 2] |= ((uint32_t)t0 & 0xFFu) << (8 * (q & 3));
+        p1[q >> 2] |= ((uint32_t)t1 & 0xFFu) << (8 * (q & 3));
+      }
+      *reinterpret_cast<uint4*>(xq + G * 32) = uint4{p0[0], p0[1], p0[2], p0[3]};
+      *reinterpret_cast<uint4*>(xq + G * 32 + 16) = uint4{p1[0], p1[1], p1[2], p1[3]};
+      xs[G] = float2{s0, sum};
+    }
+    TRACE(1);
+    if (tid == 0) ok_flag = 1;
+    if (wave == 0) {
+      if (!route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+        if (lane == 0) ok_flag = 0, fail(a.err);
+      } else if (a.has_sh && lane == 0) {
+        const float z = __uint_as_float(ld_sc1(a.fs + FS_LOGITS + a.E));
+        sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(z) : 1.f;
+      }
+    }
+    __syncthreads();  // routing and the x image ready
+    TRACE(2);
+    if (ok_flag) {
+      const int slot = gid / nGI, urow = gid - slot * nGI;
+      const bool sh = slot >= a.k;
+      const int mat = wave >> 1, half = wave & 1;
+      const int e = sh ? 0 : sel_i[slot];
+      const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]);
+      const size_t rb = (size_t)nsbH * 144;
+      uint4 ch[kQ4GuIt];
+      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch);
+      const float r = region_dot<kQ4GuIt>(ch, nsbH, xq, xs, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64,
+                                          reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16,
+                                          reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576);
+      if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r;
+      TRACE(3);
+      __syncthreads();
+      if (wave == 0 && lane < 16) {
+        const int rr = urow * 16 + lane;
+        float g = gu_part[0][lane], u = gu_part[1][lane];
+        if (!sh && a.gate_b) g = g + a.gate_b[(size_t)e * a.I + rr];
+        if (!sh && a.up_b) u = u + a.up_b[(size_t)e * a.I + rr];
+        const float hact = (!sh && a.act == MR_ACT_SWIGLU_OAI) ? swiglu_oai(g, u, a.alpha, a.limit) : silu_mul(g, u);
+        const float h = hact * sel_w[slot];
+        float m = max8(fabsf(h));
+        m = fmaxf(m, dpp_f<kDppMirror>(m));
+        float sum = sum8(h);
+        sum = sum + dpp_f<kDppMirror>(sum);
+        int t0, t1;
+        float s0;
+        split_i8(h, m, t0, t1, s0);
+        hb[lane] = (int8_t)t0, hb[16 + lane] = (int8_t)t1;
+        lds_drain();
+        __builtin_amdgcn_wave_barrier();
+        const size_t blk = (size_t)slot * nGI + urow;
+        if (lane < 8) st_sc1(a.himg + blk * 8 + lane, reinterpret_cast<const uint32_t*>(hb)[lane]);
+        if (lane == 0) st_sc1(reinterpret_cast<uint32_t*>(a.hsc) + blk * 2, __float_as_uint(s0));
+        if (lane == 1) st_sc1(reinterpret_cast<uint32_t*>(a.hsc) + blk * 2 + 1, __float_as_uint(sum));
+        vm_drain();  // image stores complete before the count that announces them
+      }
+      TRACE(4);
+    }
+    // counted even when routing failed, so later launches stay in step
+    if (tid == 0) count(a.fs + FS_GU, gid);
+  } else {
+    // ------------------------------------------------------------- down
+    const int q = bid - a.R;
+    if (tid == 0) ok_flag = 1;
+    if (wave == 0) {
+      if (!route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+        if (lane == 0) ok_flag = 0, fail(a.err);
+      }
+    }
+    __syncthreads();
+    TRACE(1);
+    if (ok_flag) {
+      const size_t rb = (size_t)nsbI * 144;
+      uint4 ch[kQ4DnSlots][kQ4DnIt];
+#pragma unroll
+      for (int j = 0; j < kQ4DnSlots; ++j) {
+        const int s = wave + 4 * j;
+        const int sc = s < a.ktot ? s : 0;
+        const uint8_t* D = sc >= a.k ? a.sh_down : a.down + a.down_off[sel_i[sc]];
+        if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, nsbI, ch[j]);
+      }
+      float ybias = 0.f;  // this row's routed bias terms (layer.rs:1417-1444)
+      if (tid < 8 && a.down_b)
+        for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 8 + tid];
+      TRACE(2);
+      if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+        ok_flag = 0, fail(a.err);
+      __syncthreads();
+      TRACE(3);
+      if (ok_flag) {
+        // down input image of every slot -> LDS (agent-coherent direct-to-LDS loads)
+        uint8_t* hq = smem + kDnHq;
+        float2* hs = reinterpret_cast<float2*>(smem + kDnHs);
+        {
+          const int nq = a.ktot * nGI * 2;  // 16-byte pieces of the terms
+          const uint8_t* src = reinterpret_cast<const uint8_t*>(a.himg);
+          for (int b = wave; b * 64 < nq; b += 4) {
+            const int idx = min(b * 64 + lane, nq - 1);
+            __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, hq + b * 1024, 16, 0, 16 /* sc1 */);
+          }
+          const int ns = (a.ktot * nGI + 1) / 2;  // 16-byte pieces of the (s0, sum) pairs
+          const uint8_t* ssrc = reinterpret_cast<const uint8_t*>(a.hsc);
+          for (int b = wave; b * 64 < ns; b += 4) {
+            const int idx = min(b * 64 + lane, ns - 1);
+            __builtin_amdgcn_global_load_lds(ssrc + (size_t)idx * 16, reinterpret_cast<uint8_t*>(hs) + b * 1024, 16, 0,
+                                             16 /* sc1 */);
+          }
+          vm_drain();
+        }
+        __syncthreads();
+        TRACE(4);
+#pragma unroll
+        for (int j = 0; j < kQ4DnSlots; ++j) {
+          const int s = wave + 4 * j;
+          if (s < a.ktot) {
+            const float r = region_dot<kQ4DnIt>(ch[j], nsbI, hq + (size_t)s * nGI * 32, hs + (size_t)s * nGI,
+                                                reinterpret_cast<uint4*>(smem + kDnHraw) + wave * 24,
+                                                reinterpret_cast<float*>(smem + kDnHdec) + wave * 24 * 16,
+                                                reinterpret_cast<float*>(smem + kDnVbuf) + wave * 216);
+            if ((lane & 7) == 0) dn_part[s][lane >> 3] = r;
+            lds_drain();
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+        __syncthreads();
+        if (tid < 8) {
+          const int rr = q * 8 + tid;
+          float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
+          for (int p = 0; p < a.k; ++p) yv = yv + dn_part[sel_o[p]][tid];
+          yv = yv + ybias;
+          if (a.has_sh) yv = yv + dn_part[a.k][tid];  // shared expert after the routed sum
+          if (rr < a.H) a.y[rr] = yv;
+        }
+      }
+    }
+  }
+  // ----------------------------------------------------------------- exit
+  __syncthreads();
+  TRACE(5);
+#ifdef MR_FUSED_TRACE
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + 7] = __smid();
+#endif
+  if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
+}
+
+// Shapes the fused Q4_K kernel runs; others take the VALU path.
+bool fused_q4k_supported(const mr_layer& L, int n_cu) {
+  if (L.type != MR_GGML_Q4_K || L.H % 256 != 0 || L.I % 256 != 0) return false;
+  if (L.H > (uint32_t)kQ4MaxH || L.I > (uint32_t)kQ4MaxI || L.H > 4u * kQ4RouterVec * 64) return false;
+  const uint32_t has_sh = L.d.sh_gate ? 1u : 0u;
+  if (has_sh && (L.d.sh_gate->type != MR_GGML_Q4_K || L.d.sh_up->type != MR_GGML_Q4_K ||
+                 L.d.sh_down->type != MR_GGML_Q4_K || L.Ish != L.I))
+    return false;
+  const uint64_t ktot = L.d.top_k + has_sh;
+  if (ktot > (uint64_t)kQ4MaxSlots || L.E > 512 || L.E + has_sh > (uint32_t)kMaxLogits) return false;
+  const uint64_t R = (L.E + has_sh + 3) / 4, ND = L.H / 8, NG = ktot * (L.I / 16);
+  // every workgroup resident at once (106 VGPRs and 36 KB LDS allow 4 per CU; 3 are assumed)
+  if (R + ND + NG > 3ull * n_cu || R + ND + NG > (uint64_t)kMaxGrid) return false;
+  return true;
+}
+
+hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
+                            uint8_t* img_base) {
+  Q4Args a{};
+#ifdef MR_FUSED_TRACE
+  a.trace = g_fused_trace;
+#endif
+  a.gate = L.d.gate->base, a.up = L.d.up->base, a.down = L.d.down->base;
+  a.gate_off = L.d.gate->d_offsets, a.up_off = L.d.up->d_offsets, a.down_off = L.d.down->d_offsets;
+  a.has_sh = L.d.sh_gate ? 1 : 0;
+  if (a.has_sh) {
+    a.sh_gate = L.d.sh_gate->base + L.d.sh_gate->h_offsets[0];
+    a.sh_up = L.d.sh_up->base + L.d.sh_up->h_offsets[0];
+    a.sh_down = L.d.sh_down->base + L.d.sh_down->h_offsets[0];
+  }
+  a.gate_b = L.d.gate_bias, a.up_b = L.d.up_bias, a.down_b = L.d.down_bias;
+  a.router_w = L.d.router_w, a.router_b = L.d.router_b, a.mask = L.d.dummy_mask;
+  a.sh_gate_inp = L.d.sh_gate_inp;
+  a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
+  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)L.d.top_k, a.ktot = a.k + a.has_sh;
+  const uint64_t nGI = L.I / 16;
+  a.himg = reinterpret_cast<uint32_t*>(img_base);
+  a.hsc = reinterpret_cast<float*>(img_base + (uint64_t)a.ktot * nGI * 32);
+  a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
+  a.R = (a.E + a.has_sh + 3) / 4;
+  a.ND = (int)(L.H / 8);
+  a.NG = (int)((uint64_t)a.ktot * nGI);
+  a.spin_limit = L.ctx->spin_limit;
+  ProfScope ps(K, "fused_layer");
+  hipLaunchKernelGGL(k_fused_q4k, dim3(a.R + a.ND + a.NG), dim3(256), 0, K.s, a);
+  return hipGetLastError();
+}
+
+}  // namespace mr

@@ -138,5 +138,11 @@ bool fused_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu);
 uint64_t fused_layer_sync_bytes();
+bool fused_q4k_supported(const mr_layer& L, int n_cu);
+hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
+                            uint8_t* img_base);
+#ifdef MR_FUSED_TRACE
+extern unsigned long long* g_fused_trace;
+#endif
 
 }  // namespace mr

@@ -27,7 +27,8 @@ DEVICE_NONE = -1
 OPT_DECODE_KERNEL = 1
 OPT_PROFILE = 2
 OPT_SPIN_LIMIT = 3
-DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
+DECODE_AUTO, DECODE_VALU, DECODE_FUSED = 0, 1, 2
+DECODE_MFMA = DECODE_FUSED  # earlier name
 
 if not LIB_PATH.exists():
     raise ImportError(

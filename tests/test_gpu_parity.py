@@ -233,9 +233,13 @@ def test_graph_replay_matches_eager(gpu_ctx, layers):
         b.free()
 
 
-# ---- fused single-launch MXFP4 decode kernel -----------------------------------------
+# ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
-@pytest.mark.parametrize("name", ["tiny-mxfp4", "C1-gpt-oss"])
+FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-shared", "C3-qwen3-layer0",
+         "C4-coder-next-layer0"]
+
+
+@pytest.mark.parametrize("name", FUSED)
 def test_fused_matches_oracle_and_valu(gpu_ctx, layers, name):
     dl, host = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
@@ -246,7 +250,7 @@ def test_fused_matches_oracle_and_valu(gpu_ctx, layers, name):
     try:
         for t in range(4):
             xp = dx.ptr + t * spec.hidden * 4
-            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_MFMA)
+            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_FUSED)
             dl.layer.forward(xp, dy)
             gpu_ctx.sync()
             yf = dy.download(np.float32)
@@ -263,8 +267,9 @@ def test_fused_matches_oracle_and_valu(gpu_ctx, layers, name):
     dx.free(), dy.free()
 
 
-def test_fused_repeated_launches_are_identical(gpu_ctx, layers):
-    dl, _ = get_layer(gpu_ctx, layers, "C1-gpt-oss")
+@pytest.mark.parametrize("name", ["C1-gpt-oss", "C4-coder-next-layer0"])
+def test_fused_repeated_launches_are_identical(gpu_ctx, layers, name):
+    dl, _ = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
     x = W.x_tokens(spec, 2, first_token=60)
     dx0, dx1 = gpu_ctx.to_device(x[0]), gpu_ctx.to_device(x[1])
@@ -281,8 +286,9 @@ def test_fused_repeated_launches_are_identical(gpu_ctx, layers):
         b.free()
 
 
-def test_fused_graph_replay(gpu_ctx, layers):
-    dl, _ = get_layer(gpu_ctx, layers, "tiny-mxfp4")
+@pytest.mark.parametrize("name", ["tiny-mxfp4", "tiny-q4k-shared"])
+def test_fused_graph_replay(gpu_ctx, layers, name):
+    dl, _ = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
     dl.layer.reserve(1)
     x = W.x_tokens(spec, 1, first_token=70)
@@ -305,11 +311,12 @@ def test_fused_graph_replay(gpu_ctx, layers):
         b.free()
 
 
-def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers):
+@pytest.mark.parametrize("name", ["C1-gpt-oss", "C3-qwen3-layer0"])
+def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers, name):
     """A tiny spin limit (forced from the host) may make a cross-workgroup wait
     run out: the kernel still exits, mr_sync reports it, and the next launch
     with the default limit is correct."""
-    dl, host = get_layer(gpu_ctx, layers, "C1-gpt-oss")
+    dl, host = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
     x = W.x_tokens(spec, 1, first_token=80)
     dx, dy = gpu_ctx.to_device(x[0]), gpu_ctx.alloc(spec.hidden * 4)
