@@ -58,19 +58,20 @@ constexpr int kGuHraw = kGuXs + kQ4MaxH / 16 * 8;        // [4 waves][64 sb] raw
 constexpr int kGuHdec = kGuHraw + 4 * 64 * 16;           // [4][64 sb][16 floats] decoded
 constexpr int kGuVbuf = kGuHdec + 4 * 64 * 64;           // [4][576] chunk partials
 constexpr int kGuEnd = kGuVbuf + 4 * 576 * 4;
-// down workgroups
-constexpr int kDnGroups = kQ4MaxI / 16;
-constexpr int kDnHq = 0;                                  // [slots][I/16][32] h terms
-constexpr int kDnHs = kDnHq + kQ4MaxSlots * kDnGroups * 32;  // [slots][I/16] float2
-constexpr int kDnHraw = kDnHs + kQ4MaxSlots * kDnGroups * 8 + 1024;  // + 1 KiB load overrun
-constexpr int kDnHdec = kDnHraw + 4 * 24 * 16;
-constexpr int kDnVbuf = kDnHdec + 4 * 24 * 64;
-constexpr int kDnEnd = kDnVbuf + 4 * 216 * 4;
+// down workgroups. A wave takes ns = ceil(ktot/4) slots; per-wave header and
+// partial arrays hold ns regions of 8 rows x I/256 super-blocks: ns*I/256 <= kDnSbW/8.
+constexpr int kDnSbW = 48;                                  // super-blocks per wave (all its regions)
+constexpr int kDnHq = 0;                                    // [slots][I/16][32] h terms
+constexpr int kDnHqBytes = kQ4MaxSlots * 512 * 2;           // ktot * I * 2 <= 12 * 512 * 2
+constexpr int kDnHs = kDnHq + kDnHqBytes + 1024;            // [slots][I/16] float2 (+ 1 KiB load overrun)
+constexpr int kDnHdec = kDnHs + kDnHqBytes / 4 + 1024;      // [4 waves][kDnSbW][16 floats]
+constexpr int kDnVbuf = kDnHdec + 4 * kDnSbW * 64;          // [4][kDnSbW * 9] partials; raw headers alias it
+constexpr int kDnEnd = kDnVbuf + 4 * kDnSbW * 9 * 4;
 constexpr int kQ4Smem = kGuEnd > kDnEnd ? kGuEnd : kDnEnd;
+static_assert(kDnSbW * 9 * 4 >= kDnSbW * 16, "raw headers fit in the partials slice");
 static_assert(72 * (kQ4MaxH / 256) <= 64 * kQ4GuIt && 72 * (kQ4MaxI / 256) <= 64 * kQ4DnIt,
               "a wave's chunks cover its 8-row region");
-static_assert(72 * (kQ4MaxH / 256) <= 576 && 72 * (kQ4MaxI / 256) <= 216 && 8 * (kQ4MaxI / 256) <= 24,
-              "per-wave LDS slices hold a region's partials and headers");
+static_assert(72 * (kQ4MaxH / 256) <= 576, "per-wave LDS slices hold a gate/up region");
 
 struct Q4Args {
   const uint8_t* gate;
@@ -118,28 +119,36 @@ __device__ __forceinline__ void split_i8(float v, float m, int& t0, int& t1, flo
   t1 = (int)fminf(fmaxf(rintf(r / s1), -127.f), 127.f);
 }
 
-// ---- one region: 8 rows of a Q4_K matrix --------------------------------------------------
-// ch: the lane's chunks (chunk c = 64*i + lane of the region). nsb: super-blocks per
-// row; nch = 72*nsb. Activation image: terms `xq` ([G][32 B]) and `xs` ([G] (s0, sum)).
-// Leaves each row's dot product in lanes 8*row (row = 0..7).
-template <int IT>
-__device__ __forceinline__ float region_dot(const uint4 (&ch)[IT], int nsb, const uint8_t* xq,
-                                            const float2* xs, uint4* hraw, float* hdec, float* vbuf) {
+// ---- regions: 8 rows of a Q4_K matrix each -------------------------------------------------
+// A wave holds ns regions (slots) of nsb super-blocks per row: nch = 72*nsb
+// chunks each; chunk c = 64*i + lane of region s is ch[s][i]. Work is split in
+// phases so a wave pays one LDS drain per phase for all its regions.
+
+// Phase 1 (needs only the weights): stage each super-block's header chunk in
+// LDS (hraw), then decode it into (d*sc_j, dmin*m_j) for its 8 sub-blocks (hdec,
+// 16 floats per super-block, regions one after another).
+template <int IT, int NS>
+__device__ __forceinline__ void region_headers(const uint4 (&ch)[NS][IT], int nsb, int ns, uint4* hraw,
+                                               float* hdec) {
   const int lane = threadIdx.x & 63;
-  const int nch = 72 * nsb;
-  // stage the header chunks, then decode super-block `lane`
+  const int nch = 72 * nsb, nsbr = 8 * nsb;
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = 64 * i + lane;
-    if (c < nch && c % 9 == 0) hraw[c / 9] = ch[i];
+  for (int r = 0; r < NS; ++r) {
+    if (r < ns) {
+#pragma unroll
+      for (int i = 0; i < IT; ++i) {
+        const int c = 64 * i + lane;
+        if (c < nch && c % 9 == 0) hraw[r * nsbr + c / 9] = ch[r][i];
+      }
+    }
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
-  if (lane < 8 * nsb) {
-    const uint4 h = hraw[lane];
+  for (int b = lane; b < ns * nsbr; b += 64) {
+    const uint4 h = hraw[b];
     const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
     const uint32_t s3[3] = {h.y, h.z, h.w};
-    float4* out = reinterpret_cast<float4*>(hdec + lane * 16);
+    float4* out = reinterpret_cast<float4*>(hdec + b * 16);
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
       uint32_t sc0, m0, sc1, m1;
@@ -151,49 +160,68 @@ __device__ __forceinline__ float region_dot(const uint4 (&ch)[IT], int nsb, cons
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
+}
+
+// Phase 2: quant-chunk dot products against the activation images (xq[r]: [G][32 B]
+// int8 terms, xs[r]: [G] (s0, group sum)) into vbuf, then each row's sum; out[r]
+// is left in lanes 8*row (row = 0..7). vbuf may alias hraw (headers are decoded).
+template <int IT, int NS>
+__device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], int nsb, int ns,
+                                            const uint8_t* const (&xq)[NS], const float2* const (&xs)[NS],
+                                            const float* hdec, float* vbuf, float (&out)[NS]) {
+  const int lane = threadIdx.x & 63;
+  const int nch = 72 * nsb, nsbr = 8 * nsb;
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = 64 * i + lane;
-    if (c < nch) {
-      const int sbw = c / 9, p = c - 9 * sbw;
-      float v = 0.f;
-      if (p != 0) {
-        const int row = sbw / nsb, col = sbw - row * nsb;
-        (void)row;
-        const int pp = p - 1, jj = pp >> 1, hf = pp & 1;
-        const int G = col * 16 + jj * 4 + hf;  // low nibbles; high nibbles: G + 2
-        const uint4 l0 = *reinterpret_cast<const uint4*>(xq + G * 32);
-        const uint4 l1 = *reinterpret_cast<const uint4*>(xq + G * 32 + 16);
-        const uint4 h0 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32);
-        const uint4 h1 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32 + 16);
-        const uint32_t w[4] = {ch[i].x, ch[i].y, ch[i].z, ch[i].w};
-        const uint32_t xl0[4] = {l0.x, l0.y, l0.z, l0.w}, xl1[4] = {l1.x, l1.y, l1.z, l1.w};
-        const uint32_t xh0[4] = {h0.x, h0.y, h0.z, h0.w}, xh1[4] = {h1.x, h1.y, h1.z, h1.w};
-        int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+  for (int r = 0; r < NS; ++r) {
+    if (r < ns) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const int lo = (int)(w[d] & 0x0F0F0F0Fu), hi = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
-          a0 = __builtin_amdgcn_sdot4(lo, (int)xl0[d], a0, false);
-          a1 = __builtin_amdgcn_sdot4(lo, (int)xl1[d], a1, false);
-          b0 = __builtin_amdgcn_sdot4(hi, (int)xh0[d], b0, false);
-          b1 = __builtin_amdgcn_sdot4(hi, (int)xh1[d], b1, false);
+      for (int i = 0; i < IT; ++i) {
+        const int c = 64 * i + lane;
+        if (c < nch) {
+          const int sbw = c / 9, p = c - 9 * sbw;
+          float v = 0.f;
+          if (p != 0) {
+            const int col = sbw % nsb;
+            const int pp = p - 1, jj = pp >> 1, hf = pp & 1;
+            const int G = col * 16 + jj * 4 + hf;  // low nibbles; high nibbles: G + 2
+            const uint4 l0 = *reinterpret_cast<const uint4*>(xq[r] + G * 32);
+            const uint4 l1 = *reinterpret_cast<const uint4*>(xq[r] + G * 32 + 16);
+            const uint4 h0 = *reinterpret_cast<const uint4*>(xq[r] + (G + 2) * 32);
+            const uint4 h1 = *reinterpret_cast<const uint4*>(xq[r] + (G + 2) * 32 + 16);
+            const uint32_t w[4] = {ch[r][i].x, ch[r][i].y, ch[r][i].z, ch[r][i].w};
+            const uint32_t xl0[4] = {l0.x, l0.y, l0.z, l0.w}, xl1[4] = {l1.x, l1.y, l1.z, l1.w};
+            const uint32_t xh0[4] = {h0.x, h0.y, h0.z, h0.w}, xh1[4] = {h1.x, h1.y, h1.z, h1.w};
+            int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const int lo = (int)(w[d] & 0x0F0F0F0Fu), hi = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
+              a0 = __builtin_amdgcn_sdot4(lo, (int)xl0[d], a0, false);
+              a1 = __builtin_amdgcn_sdot4(lo, (int)xl1[d], a1, false);
+              b0 = __builtin_amdgcn_sdot4(hi, (int)xh0[d], b0, false);
+              b1 = __builtin_amdgcn_sdot4(hi, (int)xh1[d], b1, false);
+            }
+            const float2 gl = xs[r][G], gh = xs[r][G + 2];
+            const float4 dm = *reinterpret_cast<const float4*>(hdec + (r * nsbr + sbw) * 16 + 4 * jj);
+            const float xlo = gl.x * (float)a0 + (gl.x * kInv254) * (float)a1;
+            const float xhi = gh.x * (float)b0 + (gh.x * kInv254) * (float)b1;
+            v = ((dm.x * xlo - dm.y * gl.y) + dm.z * xhi) - dm.w * gh.y;
+          }
+          vbuf[r * nch + c] = v;
         }
-        const float2 gl = xs[G], gh = xs[G + 2];
-        const float4 dm = *reinterpret_cast<const float4*>(hdec + sbw * 16 + 4 * jj);
-        const float xlo = gl.x * (float)a0 + (gl.x * kInv254) * (float)a1;
-        const float xhi = gh.x * (float)b0 + (gh.x * kInv254) * (float)b1;
-        v = ((dm.x * xlo - dm.y * gl.y) + dm.z * xhi) - dm.w * gh.y;
       }
-      vbuf[c] = v;
     }
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
   // row sums: 8 lanes per row, each over every 8th chunk of the row, then DPP
   const int row = lane >> 3, j8 = lane & 7, per = 9 * nsb;
-  float s = 0.f;
-  for (int c = j8; c < per; c += 8) s += vbuf[row * per + c];
-  return sum8(s);
+#pragma unroll
+  for (int r = 0; r < NS; ++r) {
+    float sm = 0.f;
+    if (r < ns)
+      for (int c = j8; c < per; c += 8) sm += vbuf[r * nch + row * per + c];
+    out[r] = sum8(sm);
+  }
 }
 
 // Loads of one region (8 rows x nsb super-blocks at `base`); chunks past the end
@@ -307,12 +335,15 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const int e = sh ? 0 : sel_i[slot];
       const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]);
       const size_t rb = (size_t)nsbH * 144;
-      uint4 ch[kQ4GuIt];
-      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch);
-      const float r = region_dot<kQ4GuIt>(ch, nsbH, xq, xs, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64,
-                                          reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16,
-                                          reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576);
-      if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r;
+      uint4 ch[1][kQ4GuIt];
+      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
+      float* hdec = reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16;
+      region_headers<kQ4GuIt, 1>(ch, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
+      const uint8_t* const xqs[1] = {xq};
+      const float2* const xss[1] = {xs};
+      float r[1];
+      region_dots<kQ4GuIt, 1>(ch, nsbH, 1, xqs, xss, hdec, reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576, r);
+      if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r[0];
       TRACE(3);
       __syncthreads();
       if (wave == 0 && lane < 16) {
@@ -366,6 +397,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       float ybias = 0.f;  // this row's routed bias terms (layer.rs:1417-1444)
       if (tid < 8 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 8 + tid];
+      // headers of this wave's slots: independent of the gate/up results
+      const int nsw = (a.ktot - wave + 3) >> 2;  // slots of this wave: wave, wave + 4, ...
+      float* hdec = reinterpret_cast<float*>(smem + kDnHdec) + wave * kDnSbW * 16;
+      float* vbuf = reinterpret_cast<float*>(smem + kDnVbuf) + wave * kDnSbW * 9;
+      region_headers<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, reinterpret_cast<uint4*>(vbuf), hdec);
       TRACE(2);
       if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
@@ -382,10 +418,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
             const int idx = min(b * 64 + lane, nq - 1);
             __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, hq + b * 1024, 16, 0, 16 /* sc1 */);
           }
-          const int ns = (a.ktot * nGI + 1) / 2;  // 16-byte pieces of the (s0, sum) pairs
+          const int npc = (a.ktot * nGI + 1) / 2;  // 16-byte pieces of the (s0, sum) pairs
           const uint8_t* ssrc = reinterpret_cast<const uint8_t*>(a.hsc);
-          for (int b = wave; b * 64 < ns; b += 4) {
-            const int idx = min(b * 64 + lane, ns - 1);
+          for (int b = wave; b * 64 < npc; b += 4) {
+            const int idx = min(b * 64 + lane, npc - 1);
             __builtin_amdgcn_global_load_lds(ssrc + (size_t)idx * 16, reinterpret_cast<uint8_t*>(hs) + b * 1024, 16, 0,
                                              16 /* sc1 */);
           }
@@ -393,19 +429,18 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         }
         __syncthreads();
         TRACE(4);
+        const uint8_t* xqs[kQ4DnSlots];
+        const float2* xss[kQ4DnSlots];
 #pragma unroll
         for (int j = 0; j < kQ4DnSlots; ++j) {
-          const int s = wave + 4 * j;
-          if (s < a.ktot) {
-            const float r = region_dot<kQ4DnIt>(ch[j], nsbI, hq + (size_t)s * nGI * 32, hs + (size_t)s * nGI,
-                                                reinterpret_cast<uint4*>(smem + kDnHraw) + wave * 24,
-                                                reinterpret_cast<float*>(smem + kDnHdec) + wave * 24 * 16,
-                                                reinterpret_cast<float*>(smem + kDnVbuf) + wave * 216);
-            if ((lane & 7) == 0) dn_part[s][lane >> 3] = r;
-            lds_drain();
-            __builtin_amdgcn_wave_barrier();
-          }
+          const int sj = min(wave + 4 * j, a.ktot - 1);
+          xqs[j] = hq + (size_t)sj * nGI * 32, xss[j] = hs + (size_t)sj * nGI;
         }
+        float r[kQ4DnSlots];
+        region_dots<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, xqs, xss, hdec, vbuf, r);
+#pragma unroll
+        for (int j = 0; j < kQ4DnSlots; ++j)
+          if (j < nsw && (lane & 7) == 0) dn_part[wave + 4 * j][lane >> 3] = r[j];
         __syncthreads();
         if (tid < 8) {
           const int rr = q * 8 + tid;
@@ -437,6 +472,8 @@ bool fused_q4k_supported(const mr_layer& L, int n_cu) {
     return false;
   const uint64_t ktot = L.d.top_k + has_sh;
   if (ktot > (uint64_t)kQ4MaxSlots || L.E > 512 || L.E + has_sh > (uint32_t)kMaxLogits) return false;
+  // per-wave LDS slices (down): ceil(ktot/4) regions of 8 rows x I/256 super-blocks; h image
+  if ((ktot + 3) / 4 * 8 * (L.I / 256) > (uint64_t)kDnSbW || ktot * L.I * 2 > (uint64_t)kDnHqBytes) return false;
   const uint64_t R = (L.E + has_sh + 3) / 4, ND = L.H / 8, NG = ktot * (L.I / 16);
   // every workgroup resident at once (106 VGPRs and 36 KB LDS allow 4 per CU; 3 are assumed)
   if (R + ND + NG > 3ull * n_cu || R + ND + NG > (uint64_t)kMaxGrid) return false;
