@@ -98,6 +98,102 @@ def measured_traffic(config: int):
     return json.loads(f.read_text()).get(f"C{config}")
 
 
+MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 (the f8f6f4 MFMA with an fp8 B operand)
+
+
+def bench_batched(a, ctx, M, W, spec):
+    """C5: one step = one batched forward of 512 tokens through the Zipf-skewed
+    GPT-OSS-shape layer (router, top-4, grouped gate/up + SwiGLU, grouped down,
+    combine)."""
+    T = W.CONFIG_TOKENS[5]
+    K, Wm = a.steps if a.steps != 256 else 20, a.warmup
+    dl = W.DeviceLayer(ctx, spec)
+    dl.layer.reserve(T)
+    H, I = spec.hidden, spec.inter
+    x = W.x_tokens(spec, T)
+    dx, dy = ctx.to_device(x), ctx.zeros((T, H))
+    ctx.sync()
+    g = None
+    if not a.no_graph:
+        ctx.graph_begin()
+        dl.layer.forward_batched(dx, T, dy)
+        g = ctx.graph_end()
+    run = (lambda: g.launch()) if g else (lambda: dl.layer.forward_batched(dx, T, dy))
+    for _ in range(Wm):
+        run()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(K):
+        run()
+    ms = ctx.timer_stop()
+    tok_s = K * T / (ms / 1e3)
+    y = dy.download(np.float32)
+    assert np.all(np.isfinite(y)), "non-finite output"
+    log(f"timed {K} steps of {T} tokens: {ms:.2f} ms -> {tok_s:.1f} tok/s")
+    ctx.set_option(M.OPT_PROFILE, 1)
+    ctx.profile_reset()
+    P = 4
+    for _ in range(P):
+        dl.layer.forward_batched(dx, T, dy)
+    ctx.sync()
+    kern = {}
+    for name in ("router_logits", "topk", "group", "split_x", "grouped_gateup", "split_h", "grouped_down",
+                 "combine", "gateup", "down"):
+        n, tot = ctx.profile_read(name)
+        if n:
+            kern[name] = (n, tot)
+    ctx.set_option(M.OPT_PROFILE, 0)
+    log("kernels: " + ", ".join(f"{k}: n={v[0]} avg={v[1] / v[0] * 1e3:.2f}us" for k, v in kern.items()))
+    dom = max(kern, key=lambda k: kern[k][1])
+    avg_ms = kern[dom][1] / kern[dom][0]
+    pairs = T * spec.top_k
+    flops = {"grouped_gateup": 2.0 * pairs * 2 * I * H, "grouped_down": 2.0 * pairs * H * I}
+    bytes_step = W.batched_bytes(spec, T)
+    roof = None
+    if dom in flops:
+        ach = flops[dom] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": MFMA_FP8_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / MFMA_FP8_PEAK_TFLOPS, 4), "traffic": None,
+                "flops_per_launch": flops[dom], "avg_launch_us": round(avg_ms * 1e3, 2),
+                "note": "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this MFMA work"}
+    cpu = None
+    if not a.no_cpu_baseline:
+        import oracle  # test infrastructure; used here only as the timed CPU baseline
+
+        host = dict(spec=spec)
+        host.update(dl.download_quant())
+        host.update(W.float_tensors(spec))
+        L = oracle.layer_from_host(host)
+        threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
+        ns = 16
+        L.forward(x[:1], n_threads=threads)
+        t0 = time.perf_counter()
+        L.forward(x[:ns], n_threads=threads)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(ns / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on {ns} of the "
+                         f"{T} tokens"}
+    out = {
+        "metric": "expert-FFN batched/prefill tokens/s + MFMA utilisation, GPT-OSS-20B shape",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(ms / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4-weights/e4m3x4-activations/f32-acc",
+        "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1); Zipf(1.1) router skew)",
+        "config": {"workload": W.CONFIG_NAMES[5], "config_id": 5, "tokens": T, "hidden": H, "inter": I,
+                   "experts": spec.n_experts, "top_k": spec.top_k, "graph": g is not None},
+        "hbm_gbs": round(bytes_step * K / (ms / 1e3) / 1e9, 1),
+        "hbm_frac": round(bytes_step * K / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_step": bytes_step,
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    if g:
+        g.close()
+    dx.free(), dy.free()
+    dl.close()
+    ctx.close()
+
+
 def main():
     a = parse()
     if a.copy_calibration:
@@ -116,7 +212,8 @@ def main():
         ctx.set_option(M.OPT_DECODE_KERNEL, {"valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel])
     specs = W.config_layers(a.config)
     if a.config == 5:
-        log("config 5 is the batched path; use tests/bench_batched via --config 5 in a later build")
+        bench_batched(a, ctx, M, W, specs[0])
+        return
     n_layers = len(specs)
     K, Wm = a.steps, a.warmup
     n_tok = K + Wm

@@ -100,7 +100,7 @@ int upload_offsets(mr_ctx* c, mr_pack* p) {
 
 // Scratch layout for T tokens of a layer shape.
 struct ScratchPlan {
-  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, total;
+  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, grouped, total;
 };
 
 ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
@@ -116,6 +116,7 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40);
   p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
+  p.grouped = o, o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
   p.total = o;
   return p;
 }
@@ -158,6 +159,7 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   s.mfma_b = b + p.mfma_b;
   s.sync = reinterpret_cast<uint32_t*>(b + p.sync);
   s.groups = reinterpret_cast<int32_t*>(b + p.groups);
+  s.grouped = b + p.grouped;
   s.cap_tokens = nT, s.cap_k = nk, s.cap_e = nE, s.cap_i = nI, s.cap_h = nH, s.cap_ish = nS;
   return MR_OK;
 }
@@ -634,7 +636,13 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
   mr::Scratch& s = c->scratch;
   hipError_t e = mr::launch_router_logits(c->launch(), *L, x, T, s.logits);
   if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, T, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
-  if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
+  if (e == hipSuccess) {
+    if (c->decode_kernel != MR_DECODE_VALU && mr::grouped_supported(*L))
+      e = mr::launch_grouped(c->launch(), *L, x, T, s.idx, s.w, y,
+                             mr::grouped_scratch(s, s.cap_tokens, s.cap_k, s.cap_e, s.cap_i, s.cap_h));
+    else
+      e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
+  }
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch");
 }
 

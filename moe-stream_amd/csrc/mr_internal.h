@@ -30,6 +30,7 @@ struct Scratch {
   void* mfma_b = nullptr;      // MFMA B-operand images (x split / act split)
   uint32_t* sync = nullptr;    // sync words for the fused decode kernel
   int32_t* groups = nullptr;   // batched path: per-expert token lists
+  void* grouped = nullptr;     // grouped MFMA path: activation images and per-pair outputs
   uint64_t cap_tokens = 0, cap_k = 0, cap_e = 0, cap_i = 0, cap_h = 0, cap_ish = 0;
 };
 
@@ -138,6 +139,26 @@ bool fused_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu);
 uint64_t fused_layer_sync_bytes();
+
+// Scratch of the grouped multi-token MXFP4 path (device pointers; P = T * top_k pairs).
+struct GroupedScratch {
+  int32_t* pair_tok;  // [P] token of sorted pair p
+  float* pair_w;      // [P] its routing weight
+  int32_t* pair_of;   // [P] sorted index of (token, slot)
+  int32_t* exp_off;   // [E+1] pair offset of each expert
+  int32_t* tile_off;  // [E+1] 16-pair tile offset of each expert
+  uint8_t* img_x;     // [T][H/32][128] x images
+  uint32_t* sc_x;     // [T][H/32]
+  uint8_t* img_h;     // [P][I/32][128] h images
+  uint32_t* sc_h;     // [P][I/32]
+  float* hbuf;        // [P][I] gate/up results (activation x routing weight)
+  float* obuf;        // [P][H] down results
+};
+GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H);
+uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H);
+bool grouped_supported(const mr_layer& L);
+hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
+                          const float* w, float* y, const GroupedScratch& gs);
 bool fused_q4k_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
                             uint8_t* img_base);

@@ -68,6 +68,19 @@ class LayerSpec:
         return f
 
 
+def batched_bytes(spec: LayerSpec, n_tokens: int) -> int:
+    """Algorithmic bytes of one batched forward: every expert's weights and biases
+    (each read once), router weights/bias, x read once, y written once."""
+    H, I, E = spec.hidden, spec.inter, spec.n_experts
+    t = spec.ggml_type
+    b = E * (2 * S.matrix_bytes(t, I, H) + S.matrix_bytes(t, H, I))
+    if spec.expert_bias:
+        b += E * (2 * I + H) * 4
+    b += E * H * 4 + (E * 4 if spec.router_bias else 0)
+    b += 2 * n_tokens * H * 4
+    return b
+
+
 def gpt_oss(config: int, layer: int, **kw) -> LayerSpec:
     base = LayerSpec(config, layer, GGML_MXFP4, 2880, 2880, 32, 4, ROUTE_SOFTMAX_AFTER_TOPK,
                      ACT_SWIGLU_OAI, True, True)
