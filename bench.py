@@ -50,11 +50,14 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(layers, specs, n_layers_sample: int, n_tokens_sample: int, threads: int):
-    """Oracle (C restatement of the reference CPU path) on a bounded sample."""
+def cpu_baseline(layers, specs, n_layers_sample: int, threads: int, budget_s: float = 10.0):
+    """Oracle (C restatement of the reference CPU path) on a bounded sample: the
+    first n_layers_sample layers, one decode token at a time, until about
+    budget_s seconds of CPU work. Returns (layer-tokens/s, layer-tokens timed)."""
     import oracle  # test infrastructure; used here only as the timed CPU baseline
     from moe_rocm import workloads as W
 
+    per_layer = budget_s / n_layers_sample
     t_total, n_lt = 0.0, 0
     for li in range(n_layers_sample):
         dl, spec = layers[li], specs[li]
@@ -62,15 +65,17 @@ def cpu_baseline(layers, specs, n_layers_sample: int, n_tokens_sample: int, thre
         host.update(dl.download_quant())
         host.update(W.float_tensors(spec))
         L = oracle.layer_from_host(host)
-        x = W.x_tokens(spec, n_tokens_sample)
+        x = W.x_tokens(spec, 1024)
         L.forward(x[:1], n_threads=threads)  # warm-up
         t0 = time.perf_counter()
-        for t in range(n_tokens_sample):
+        t = 0
+        while t < len(x) and time.perf_counter() - t0 < per_layer:
             L.forward(x[t:t + 1], n_threads=threads)
+            t += 1
         t_total += time.perf_counter() - t0
-        n_lt += n_tokens_sample
+        n_lt += t
         del host, L
-    return n_lt / t_total  # layer-tokens per second
+    return n_lt / t_total, n_lt
 
 
 def copy_calibration(n_bytes: int = 1 << 30, reps: int = 4) -> None:
@@ -165,10 +170,12 @@ def bench_batched(a, ctx, M, W, spec):
         host.update(W.float_tensors(spec))
         L = oracle.layer_from_host(host)
         threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
-        ns = 16
         L.forward(x[:1], n_threads=threads)
         t0 = time.perf_counter()
-        L.forward(x[:ns], n_threads=threads)
+        ns = 0
+        while ns < T and time.perf_counter() - t0 < 10.0:  # about 10 s of CPU work
+            L.forward(x[ns:ns + 8], n_threads=threads)
+            ns += 8
         dt = time.perf_counter() - t0
         cpu = {"value": round(ns / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
                "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on {ns} of the "
@@ -309,13 +316,13 @@ def main():
     cpu = None
     if not a.no_cpu_baseline:
         threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
-        nls, nts = (2, 24) if s0.mxfp4 else (2, 8)
+        nls = min(2, n_layers)
         t0 = time.perf_counter()
-        lt_s = cpu_baseline(layers, specs, min(nls, n_layers), nts, threads)
-        log(f"cpu baseline: {lt_s:.1f} layer-tok/s in {time.perf_counter() - t0:.1f}s")
-        cpu = {"value": lt_s / n_layers, "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on "
-                         f"{min(nls, n_layers)} of {n_layers} layers x {nts} tokens; "
+        lt_s, n_lt = cpu_baseline(layers, specs, nls, threads)
+        log(f"cpu baseline: {lt_s:.1f} layer-tok/s ({n_lt} layer-tokens) in {time.perf_counter() - t0:.1f}s")
+        cpu = {"value": round(lt_s / n_layers, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"oracle (C restatement of the reference CPU path, {threads} threads), one decode token "
+                         f"at a time, on {nls} of the {n_layers} layers for ~10 s ({n_lt} layer-tokens); "
                          f"tokens/s = layer-tokens/s / {n_layers}"}
 
     out = {
