@@ -119,7 +119,9 @@ int mr_pack_upload(mr_ctx* ctx, int ggml_type, const void* host_bytes, uint64_t 
                    uint32_t n_experts, uint32_t out_features, uint32_t in_features,
                    const uint64_t* host_offsets, mr_pack** out);
 /* Same over device bytes the caller owns and keeps alive (zero copy; the
- * reference's Mxfp4Packed views, cache.rs:289-308). */
+ * reference's Mxfp4Packed views, cache.rs:289-308). The kernels read whole
+ * aligned 16-byte pieces, so the allocation must stay readable for 64 bytes past
+ * the last expert's last block (mr_pack_upload allocates that slack itself). */
 int mr_pack_wrap(mr_ctx* ctx, int ggml_type, const void* dev_bytes, uint64_t nbytes,
                  uint32_t n_experts, uint32_t out_features, uint32_t in_features,
                  const uint64_t* host_offsets, mr_pack** out);

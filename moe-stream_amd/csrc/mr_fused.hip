@@ -115,6 +115,84 @@ __device__ __forceinline__ void issue_rows(const uint8_t* W, int S, int nb, int 
   }
 }
 
+// ---- gate/up weight stream through LDS --------------------------------------------------------
+// A wave's 16-row tile (rows adjacent in memory, rb bytes apart) is streamed in chunks of
+// kStreamSteps K steps = 4*kStreamSteps blocks: each row's chunk is fetched as kRowPieces
+// 16-byte pieces from the 16-byte aligned address at or below its first byte, by direct
+// global->LDS loads whose LDS destination is piece index * 16 (lane-contiguous), so one wave
+// load covers about four rows' contiguous bytes instead of sixteen scattered windows. The
+// MFMA A windows are read back from LDS. Two buffers per wave: chunk c+1 streams in while
+// chunk c is multiplied.
+constexpr int kStreamSteps = 3;
+constexpr int kRowPieces = 15;                    // row slot: 240 bytes
+constexpr int kStageLoads = 4;                    // wave loads per chunk (64 pieces each)
+constexpr int kStageBytes = kStageLoads * 1024;   // one buffer (pieces past 16 rows land in its pad)
+constexpr int kStageOff = 96 * kImgBytes;         // after the largest x image (H <= 3072)
+constexpr int kMaxChunks = (kSteps + kStreamSteps - 1) / kStreamSteps;
+static_assert(16 * kRowPieces <= kStageLoads * 64, "a chunk's pieces fit one buffer");
+static_assert(15 + 17 * 4 * kStreamSteps + 3 <= 16 * kRowPieces, "a row slot holds the chunk and its window tail");
+static_assert(kStageOff + 4 * 2 * kStageBytes <= 4 * kImgVec * 1024, "stage buffers fit the dynamic LDS");
+
+__device__ __forceinline__ void stream_issue(const uint8_t* W, uint64_t rb, int nb, int c, uint8_t* buf,
+                                             int lane) {
+  const int b0 = 4 * kStreamSteps * c;
+#pragma unroll
+  for (int it = 0; it < kStageLoads; ++it) {
+    const int q = it * 64 + lane;
+    const int row = min(q / kRowPieces, 15);
+    const int pc = min(q - row * kRowPieces, kRowPieces - 1);
+    const uint8_t* rs = W + (uint64_t)row * rb;
+    const uintptr_t first = reinterpret_cast<uintptr_t>(rs + (size_t)b0 * 17) & ~(uintptr_t)15;
+    const uintptr_t last = (reinterpret_cast<uintptr_t>(rs + (size_t)nb * 17) - 1) & ~(uintptr_t)15;
+    const uintptr_t src = min(first + 16 * (uintptr_t)pc, last);  // never past the row's last piece
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), buf + it * 1024, 16, 0, 0);
+  }
+}
+
+// D of one 16-row tile over all K steps: A streamed through `stage` (two kStageBytes buffers
+// of this wave), B from an x image in LDS. W: row 0 of the tile.
+__device__ __forceinline__ f32x4 stream_chain(const uint8_t* W, uint64_t rb, int S, int nb, uint8_t* stage,
+                                              const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
+                                              int lane, int i, int g) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int nc = (S + kStreamSteps - 1) / kStreamSteps;
+  const uintptr_t rs = reinterpret_cast<uintptr_t>(W + (uint64_t)i * rb);  // this lane's row
+  stream_issue(W, rb, nb, 0, stage, lane);
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    if (c < nc) {
+      if (c + 1 < nc) {
+        stream_issue(W, rb, nb, c + 1, stage + ((c + 1) & 1) * kStageBytes, lane);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStageLoads) : "memory");  // chunk c has landed
+      } else {
+        vm_drain();
+      }
+      __builtin_amdgcn_wave_barrier();
+      const uint8_t* buf = stage + (c & 1) * kStageBytes;
+      const int b0 = 4 * kStreamSteps * c;
+      const int lead = (int)((rs + (uintptr_t)b0 * 17) & 15u);  // row chunk start within its first piece
+#pragma unroll
+      for (int s = 0; s < kStreamSteps; ++s) {
+        const int st = kStreamSteps * c + s;
+        if (st < S) {
+          const int b = 4 * st + g;
+          const int off = i * (kRowPieces * 16) + lead + (b - b0) * 17;
+          const uint32_t* wp = reinterpret_cast<const uint32_t*>(buf + (off & ~3));
+          RawBlk r;
+          r.d[0] = wp[0], r.d[1] = wp[1], r.d[2] = wp[2], r.d[3] = wp[3], r.d[4] = wp[4];
+          i32x8 B;
+          int sb;
+          load_b(img, sc, zero, st, nb, i, g, B, sb);
+          acc = mfma_raw(r, (uint32_t)off & 3u, b < nb, B, sb, acc);
+        }
+      }
+      lds_drain();  // this buffer is refilled by the next iteration's stream_issue
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  return acc;
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   extern __shared__ __align__(16) uint8_t lds_dyn[];
@@ -213,13 +291,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const float wsl = sel_w[slot];
       const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
       const int S = (nbH + 3) >> 2;
-      const int row = pair * 32 + tile * 16 + i;
       const uint64_t rb = (uint64_t)nbH * 17;
-      const uint8_t* W = (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]) + (uint64_t)row * rb;
-      const uint32_t shw = (uint32_t)reinterpret_cast<uintptr_t>(W) & 3u;
-      RawBlk rw[kSteps];
-      issue_rows(W, S, nbH, g, rw);
-      f32x4 dacc = mfma_chain(rw, shw, S, nbH, lds_img, lds_sc, lds_zero, i, g, f32x4{0.f, 0.f, 0.f, 0.f});
+      const uint8_t* W = (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]) + (uint64_t)(pair * 32 + tile * 16) * rb;
+      f32x4 dacc = stream_chain(W, rb, S, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
+                                lds_zero, lane, i, g);
       TRACE(3);
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
