@@ -88,17 +88,27 @@ struct FusedArgs {
 __device__ __forceinline__ f32x4 mfma_chain(const RawBlk (&rw)[kSteps], uint32_t sh, int S, int nb,
                                             const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
                                             int i, int g, f32x4 acc) {
+  // Every one of the kSteps steps is issued, with no branch between them, so the LDS
+  // operand loads of later steps can be scheduled ahead: steps at or past S read the
+  // zero B line (and issue_rows zeroed their A), so they add exactly 0.
+  // Step j+1's B operand is loaded before step j's MFMA is issued.
+  (void)S;
+  f32x4 acc1 = {0.f, 0.f, 0.f, 0.f};  // odd steps: two independent MFMA dependency chains
+  i32x8 Bn;
+  int sbn;
+  load_b(img, sc, zero, 0, nb, i, g, Bn, sbn);
 #pragma unroll
   for (int j = 0; j < kSteps; ++j) {
-    if (j < S) {
-      i32x8 B;
-      int sb;
-      load_b(img, sc, zero, j, nb, i, g, B, sb);
-      const int c = 4 * j + g;
+    const i32x8 B = Bn;
+    const int sb = sbn;
+    if (j + 1 < kSteps) load_b(img, sc, zero, j + 1, nb, i, g, Bn, sbn);
+    const int c = 4 * j + g;
+    if (j & 1)
+      acc1 = mfma_raw(rw[j], (sh + (uint32_t)min(c, nb - 1)) & 3u, c < nb, B, sb, acc1);
+    else
       acc = mfma_raw(rw[j], (sh + (uint32_t)min(c, nb - 1)) & 3u, c < nb, B, sb, acc);
-    }
   }
-  return acc;
+  return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
 }
 
 // A operands (raw windows) of one 16-row tile, all K steps (S is wave-uniform).
@@ -154,7 +164,7 @@ __device__ __forceinline__ void stream_issue(const uint8_t* W, uint64_t rb, int 
 __device__ __forceinline__ f32x4 stream_chain(const uint8_t* W, uint64_t rb, int S, int nb, uint8_t* stage,
                                               const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
                                               int lane, int i, int g) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd steps
   const int nc = (S + kStreamSteps - 1) / kStreamSteps;
   const uintptr_t rs = reinterpret_cast<uintptr_t>(W + (uint64_t)i * rb);  // this lane's row
   stream_issue(W, rb, nb, 0, stage, lane);
@@ -171,26 +181,33 @@ __device__ __forceinline__ f32x4 stream_chain(const uint8_t* W, uint64_t rb, int
       const uint8_t* buf = stage + (c & 1) * kStageBytes;
       const int b0 = 4 * kStreamSteps * c;
       const int lead = (int)((rs + (uintptr_t)b0 * 17) & 15u);  // row chunk start within its first piece
+      // all kStreamSteps steps, unguarded: steps past S read the zero B line and add 0
+      RawBlk r[kStreamSteps];
+      i32x8 B[kStreamSteps];
+      int sb[kStreamSteps], off[kStreamSteps];
+#pragma unroll
+      for (int s = 0; s < kStreamSteps; ++s) {  // every operand of the chunk is loaded first
+        const int st = kStreamSteps * c + s;
+        const int b = 4 * st + g;
+        off[s] = i * (kRowPieces * 16) + lead + (b - b0) * 17;
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(buf + (off[s] & ~3));
+        r[s].d[0] = wp[0], r[s].d[1] = wp[1], r[s].d[2] = wp[2], r[s].d[3] = wp[3], r[s].d[4] = wp[4];
+        load_b(img, sc, zero, st, nb, i, g, B[s], sb[s]);
+      }
 #pragma unroll
       for (int s = 0; s < kStreamSteps; ++s) {
         const int st = kStreamSteps * c + s;
-        if (st < S) {
-          const int b = 4 * st + g;
-          const int off = i * (kRowPieces * 16) + lead + (b - b0) * 17;
-          const uint32_t* wp = reinterpret_cast<const uint32_t*>(buf + (off & ~3));
-          RawBlk r;
-          r.d[0] = wp[0], r.d[1] = wp[1], r.d[2] = wp[2], r.d[3] = wp[3], r.d[4] = wp[4];
-          i32x8 B;
-          int sb;
-          load_b(img, sc, zero, st, nb, i, g, B, sb);
-          acc = mfma_raw(r, (uint32_t)off & 3u, b < nb, B, sb, acc);
-        }
+        const int b = 4 * st + g;
+        if (st & 1)
+          acc1 = mfma_raw(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc1);
+        else
+          acc = mfma_raw(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc);
       }
       lds_drain();  // this buffer is refilled by the next iteration's stream_issue
       __builtin_amdgcn_wave_barrier();
     }
   }
-  return acc;
+  return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
 }
 
 // ---- the kernel ----------------------------------------------------------------------------
@@ -354,6 +371,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       float ybias = 0.f;
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
+      const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
       TRACE(2);
       if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
@@ -377,12 +395,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
             const uint32_t sc1v = ld_sc1(a.dsc + slot * nbI + min(lane + 64, nbI - 1));
             if (lane < nbI) wsc[lane] = sc0;
             if (lane + 64 < nbI) wsc[lane + 64] = sc1v;
-            vm_drain();
+            vm_drain();  // the slot image has landed in LDS
             __builtin_amdgcn_wave_barrier();
           }
           TRACE(4);
-          const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
+          XTRACE(wave);  // per wave: image in LDS
           d = mfma_chain(rd, sh, S, nbI, wimg, wsc, lds_zero, i, g, d);
+          XTRACE(4 + wave);  // per wave: chain done
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -396,6 +415,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           for (int p = 0; p < a.k; ++p) yv = yv + lds_part[sel_o[p] * 16 + tid];
           yv = yv + ybias;
           if (rr < a.H) a.y[rr] = yv;
+          XTRACE(8);
         }
       }
     }
@@ -404,7 +424,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   __syncthreads();
   TRACE(5);
 #ifdef MR_FUSED_TRACE
-  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + 7] = __smid();
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
 #endif
   if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
 }

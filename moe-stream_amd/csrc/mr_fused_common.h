@@ -39,17 +39,24 @@ __device__ __forceinline__ uint32_t* wg_seq_word(uint32_t* fs) { return fs + FS_
 #ifdef MR_FUSED_TRACE
 #define TRACE(slot)                                                                       \
   do {                                                                                    \
-    if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + (slot)] = wall_clock64(); \
+    if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + (slot)] = wall_clock64(); \
+  } while (0)
+#define XTRACE(slot)                                                                              \
+  do {                                                                                            \
+    if (a.trace && (threadIdx.x & 63) == 0) a.trace[blockIdx.x * 32 + 16 + (slot)] = wall_clock64(); \
   } while (0)
 #define RTRACE(slot)                                                                             \
   do {                                                                                           \
-    if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 16 + 8 + (slot)] = wall_clock64(); \
+    if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 32 + 8 + (slot)] = wall_clock64(); \
   } while (0)
 #else
 #define TRACE(slot) \
   do {              \
   } while (0)
 #define RTRACE(slot) \
+  do {               \
+  } while (0)
+#define XTRACE(slot) \
   do {               \
   } while (0)
 #endif

@@ -457,7 +457,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   __syncthreads();
   TRACE(5);
 #ifdef MR_FUSED_TRACE
-  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 16 + 7] = __smid();
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
 #endif
   if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
 }

@@ -74,7 +74,10 @@ __device__ __forceinline__ void load_b(const uint8_t* img, const uint32_t* sc, c
   const i32x4 v1 = *reinterpret_cast<const i32x4*>(p1);
   B = i32x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
   const int bs = min(4 * st + g, nb - 1);
-  sb = col ? (int)((sc[bs] >> (8 * (i & 3))) & 0xFFu) : 127;
+  // Columns past kTerms multiply a zero B operand, so any finite scale serves them: every
+  // lane takes a byte of the block's scale word (bytes are <= 247, never the NaN code 0xFF),
+  // with no branch around the LDS load.
+  sb = (int)((sc[bs] >> (8 * (i & 3))) & 0xFFu);
 }
 
 // Raw 20-byte window (5 aligned dwords) holding one 17-byte block.
@@ -86,6 +89,33 @@ __device__ __forceinline__ void raw_load(const uint8_t* p, RawBlk& r) {
   r.d[0] = w[0], r.d[1] = w[1], r.d[2] = w[2], r.d[3] = w[3], r.d[4] = w[4];
 }
 __device__ __forceinline__ void raw_zero(RawBlk& r) { r.d[0] = r.d[1] = r.d[2] = r.d[3] = r.d[4] = 0u; }
+
+// A operand of one lane from a raw block window (sh = block address & 3; the 16 code
+// bytes start at byte sh+1): the 4 code dwords and the e8m0 scale byte. An invalid
+// block (past the row end) becomes all-zero codes, so it adds exactly 0 whatever B holds
+// (as long as B is finite).
+struct AOp {
+  uint32_t q[4];
+};
+__device__ __forceinline__ AOp prep_a(const RawBlk& r, uint32_t sh, bool valid, int& sa) {
+  const uint32_t t = sh + 1u;
+  AOp a;
+  if (t == 4u) {
+    a.q[0] = r.d[1], a.q[1] = r.d[2], a.q[2] = r.d[3], a.q[3] = r.d[4];
+  } else {
+    a.q[0] = __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
+    a.q[1] = __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
+    a.q[2] = __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
+    a.q[3] = __builtin_amdgcn_alignbyte(r.d[4], r.d[3], t);
+  }
+  sa = valid ? (int)((r.d[0] >> (8u * sh)) & 0xFFu) : 127;
+  if (!valid) a.q[0] = a.q[1] = a.q[2] = a.q[3] = 0u;
+  return a;
+}
+__device__ __forceinline__ f32x4 mfma_op(const AOp& a, int sa, const i32x8& B, int sb, f32x4 acc) {
+  const i32x8 A = {(int)a.q[0], (int)a.q[1], (int)a.q[2], (int)a.q[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
+}
 
 // One MFMA on a raw block window; sh = block address & 3. The 16 code bytes
 // start at byte sh+1 of the window.
@@ -106,4 +136,16 @@ __device__ __forceinline__ f32x4 mfma_raw(const RawBlk& r, uint32_t sh, bool val
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
 }
 
+// B operand for a prepared-A chain: column i reads term i%4 (columns 4..15 repeat
+// the terms; only columns 0..3 are summed afterwards, and the data is finite), block
+// indices clamp to the last block (the A operand of an invalid block is zero).
+// base = image + (i%4)*32 + 16*(g&1) of this lane.
+__device__ __forceinline__ void load_b_fast(const uint8_t* base, const uint32_t* sc, int st, int nb, int i,
+                                            int g, i32x8& B, int& sb) {
+  const int b0 = min(4 * st + (g >> 1), nb - 1), b1 = min(4 * st + 2 + (g >> 1), nb - 1);
+  const i32x4 v0 = *reinterpret_cast<const i32x4*>(base + b0 * kImgBytes);
+  const i32x4 v1 = *reinterpret_cast<const i32x4*>(base + b1 * kImgBytes);
+  B = i32x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  sb = (int)((sc[min(4 * st + g, nb - 1)] >> (8 * (i & 3))) & 0xFFu);
+}
 }  // namespace mr
