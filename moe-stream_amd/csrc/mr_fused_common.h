@@ -220,21 +220,24 @@ __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, 
     const int e = lane + 64 * j;
     v[j] = (j < nj && e < rc.E) ? __uint_as_float(ld_sc1(rc.fs + FS_LOGITS + e)) : -INFINITY;
   }
-  const bool softmax_after = (rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
-  if (!softmax_after) {  // rank by probability: softmax over all experts first
+  // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen
+  // mode; exp is monotonic, so the order differs only where two logits round to the
+  // same probability (a tie by value, which the tests treat as ambiguous).
+  // Weights: GPT-OSS (softmax over the k) and renormalised Qwen routing are the same
+  // softmax over the k selected logits; plain Qwen routing needs the all-expert sum.
+  const bool sel_softmax = (rc.flags & (MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK)) != 0u;
+  float m_all = 0.f, s_all = 1.f;
+  if (!sel_softmax) {
     RTRACE(2);
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kRouteVals; ++j) m = fmaxf(m, v[j]);
-    m = wave_max_f(m);
+    m_all = wave_max_f(m);
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < kRouteVals; ++j)
-      if (lane + 64 * j < rc.E) s += __expf(v[j] - m);
-    s = wave_sum_f(s);
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j)
-      if (lane + 64 * j < rc.E) v[j] = __expf(v[j] - m) / s;
+      if (lane + 64 * j < rc.E) s += __expf(v[j] - m_all);
+    s_all = wave_sum_f(s);
   }
   RTRACE(3);
   uint32_t key[kRouteVals];
@@ -274,15 +277,16 @@ __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, 
     }
   }
   RTRACE(5);
-  // weights over the k selected values (lane r = slot r, in selection order)
+  // weights over the k selected logits (lane r = slot r, in selection order)
   const bool in = lane < rc.k;
-  float w = in ? key_value(my_key) : 0.f;
-  if (softmax_after) {
-    const float m = lane_f<0>(w);  // slot 0 holds the largest value
-    const float ex = in ? __expf(w - m) : 0.f;
+  const float l = in ? key_value(my_key) : 0.f;
+  float w;
+  if (sel_softmax) {
+    const float m = lane_f<0>(l);  // slot 0 holds the largest logit
+    const float ex = in ? __expf(l - m) : 0.f;
     w = ex / wave_sum_f(ex);
-  } else if (rc.flags & MR_ROUTE_NORM_TOPK) {
-    w = w / wave_sum_f(w);
+  } else {
+    w = __expf(l - m_all) / s_all;
   }
   int p = 0;  // position of this slot's expert in ascending expert order
 #pragma unroll

@@ -171,6 +171,8 @@ __device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], int nsb, 
                                             const float* hdec, float* vbuf, float (&out)[NS]) {
   const int lane = threadIdx.x & 63;
   const int nch = 72 * nsb, nsbr = 8 * nsb;
+  // sbw / nsb for sbw < 64 as a multiply: (sbw * ceil(2^16 / nsb)) >> 16 is exact there
+  const uint32_t inv_nsb = (65536u + (uint32_t)nsb - 1u) / (uint32_t)nsb;
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
     if (r < ns) {
@@ -181,7 +183,7 @@ __device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], int nsb, 
           const int sbw = c / 9, p = c - 9 * sbw;
           float v = 0.f;
           if (p != 0) {
-            const int col = sbw % nsb;
+            const int col = sbw - (int)(((uint32_t)sbw * inv_nsb) >> 16) * nsb;
             const int pp = p - 1, jj = pp >> 1, hf = pp & 1;
             const int G = col * 16 + jj * 4 + hf;  // low nibbles; high nibbles: G + 2
             const uint4 l0 = *reinterpret_cast<const uint4*>(xq[r] + G * 32);
@@ -339,10 +341,12 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
       float* hdec = reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16;
       region_headers<kQ4GuIt, 1>(ch, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
+      XTRACE(wave);  // per wave: weights landed, headers decoded
       const uint8_t* const xqs[1] = {xq};
       const float2* const xss[1] = {xs};
       float r[1];
       region_dots<kQ4GuIt, 1>(ch, nsbH, 1, xqs, xss, hdec, reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576, r);
+      XTRACE(4 + wave);  // per wave: dot products done
       if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r[0];
       TRACE(3);
       __syncthreads();

@@ -109,7 +109,9 @@ def coder_next(config: int, layer: int, n_experts: int | None = None, **kw) -> L
 def config_layers(config: int) -> list[LayerSpec]:
     """All layers of a configured workload (C1..C5)."""
     if config == 1:
-        return [gpt_oss(1, 0)]
+        # one layer shape; 8 independently seeded instances (3.4 GB) are cycled so the
+        # 256 MB Infinity Cache cannot serve repeats
+        return [gpt_oss(1, l) for l in range(8)]
     if config == 2:
         return [gpt_oss(2, l) for l in range(24)]
     if config == 3:

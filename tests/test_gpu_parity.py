@@ -94,8 +94,10 @@ TINY_Q4 = W.LayerSpec(202, 0, W.GGML_Q4_K, 1024, 512, 16, 4, W.ROUTE_NORM_TOPK, 
                       False, False)
 TINY_SH = W.LayerSpec(203, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
                       False, False, sh_inter=256)
+TINY_Q4P = W.LayerSpec(204, 0, W.GGML_Q4_K, 512, 256, 12, 3, 0, W.ACT_SILU, False, False)  # plain softmax
 SPECS = {
     "tiny-mxfp4": TINY_MX,
+    "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
     "tiny-q4k-shared": TINY_SH,
     "C1-gpt-oss": W.gpt_oss(1, 0),
@@ -274,7 +276,7 @@ def test_graph_replay_matches_eager(gpu_ctx, layers):
 
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
-FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-shared", "C3-qwen3-layer0",
+FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
          "C4-coder-next-layer0"]
 
 
