@@ -5,13 +5,13 @@
 // the expert's tokens, gate/up/act/down, x routing weight, index_add back
 // (layer.rs:2148-2183; CPU: mxfp4_matmul per expert, layer.rs:1449-1514). Here:
 //   k_group       (token, slot) pairs sorted by (expert, token, slot); per-expert
-//                 pair offsets and 16-pair tile offsets; pair index of every
+//                 pair offsets and 32-pair tile offsets; pair index of every
 //                 (token, slot).
 //   k_split_rows  activation rows -> e4m3 B images (4 terms per 32-element block).
-//   k_grouped_gemm<true>   gate and up for one (expert, 64-row tile, 16-pair tile):
+//   k_grouped_gemm<true>   gate and up for one (expert, 64-row tile, 32-pair tile):
 //                 A = native MXFP4 weight rows, B = the 16 pairs' x images; epilogue
 //                 bias + activation x routing weight -> h [pair][I].
-//   k_grouped_gemm<false>  down for one (expert, 64-row tile, 16-pair tile) on the
+//   k_grouped_gemm<false>  down for one (expert, 128-row tile, 32-pair tile) on the
 //                 h images -> o [pair][H].
 //   k_combine     y[t] = sum over t's pairs in ascending expert order of
 //                 (o + w*b_down) (the order of layer.rs:1092-1106).
@@ -27,8 +27,7 @@
 
 namespace mr {
 
-constexpr int kPairTile = 16;   // pairs (tokens) per workgroup tile = 4 MFMA column groups x 4
-constexpr int kRowTile = 64;    // output rows per workgroup tile = 4 waves x 16
+constexpr int kPairTile = 32;   // pairs (tokens) per work item = 8 MFMA column groups x 4
 constexpr int kXcds = 8;        // MI355X accelerator complex dies (one L2 each)
 constexpr int kMaxSteps = 32;   // K steps (4 blocks) per row: K <= 4096
 
@@ -116,47 +115,37 @@ struct GroupedArgs {
   float alpha, limit;
 };
 
-// One K step's operands for a wave: A raw windows of its 16 rows (gate, up), and
-// the B operands of the 4 pair groups (lane (i, g) -> pair 4c + i/4, term i%4).
-template <int NM>
-struct StepOps {
-  RawBlk a[NM];
-  i32x8 b[4];
-  int sb[4];
-};
+// Grouped GEMM work item: (expert e, row tile, 32-pair tile). 8 waves; each wave owns
+// 16 output rows of one matrix (gate/up: waves 0-3 gate, 4-7 up, the same 64 rows;
+// down: 8 x 16 = 128 rows) and all 32 pairs (8 MFMA column groups of 4 pairs x 4 terms).
+// K advances one MFMA step (4 blocks) at a time through double-buffered LDS:
+//   B: the step's 32 pairs x 4 blocks x 128-byte images (16 KB), loaded cooperatively
+//      by direct global->LDS loads (each pair's 512 bytes are contiguous) and shared
+//      by the 8 waves;
+//   A: each wave's 16 rows x 68 bytes, fetched as 6 aligned 16-byte pieces per row by
+//      direct global->LDS loads (rows are 1530 bytes apart, so a wave load covers ~10
+//      rows' contiguous bytes instead of 16 scattered block windows).
+constexpr int kGemmWaves = 8;
+constexpr int kAPieces = 6;                         // pieces per row and step: 15 + 68 + 3 <= 96
+constexpr int kAStage = 2 * 1024;                   // one A buffer: 96 pieces + pad (2 wave loads)
+constexpr int kBStage = kPairTile * 4 * kImgBytes;  // one B buffer: 32 pairs x 4 blocks
+static_assert(kPairTile * 4 * 8 == 2 * 512, "two B pieces per thread per step");
 
-template <int NM>
-__device__ __forceinline__ void load_step(StepOps<NM>& o, int st, int nbK, int g, int t,
-                                          const uint8_t* const (&wrow)[NM], const uint8_t* const (&bsrc)[4],
-                                          const uint32_t* const (&bsc)[4]) {
-  const int ab = min(4 * st + g, nbK - 1);
-#pragma unroll
-  for (int m = 0; m < NM; ++m) raw_load(wrow[m] + (size_t)ab * 17, o.a[m]);
-  const int b0 = 4 * st + (g >> 1), b1 = b0 + 2;
-  const bool v0 = b0 < nbK, v1 = b1 < nbK;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const i32x4 x0 = *reinterpret_cast<const i32x4*>(bsrc[c] + (size_t)min(b0, nbK - 1) * kImgBytes);
-    const i32x4 x1 = *reinterpret_cast<const i32x4*>(bsrc[c] + (size_t)min(b1, nbK - 1) * kImgBytes);
-    o.b[c] = i32x8{v0 ? x0[0] : 0, v0 ? x0[1] : 0, v0 ? x0[2] : 0, v0 ? x0[3] : 0,
-                   v1 ? x1[0] : 0, v1 ? x1[1] : 0, v1 ? x1[2] : 0, v1 ? x1[3] : 0};
-    o.sb[c] = (int)((bsc[c][ab] >> (8 * t)) & 0xFFu);
-  }
-}
-
-// One (expert, 64-row tile, 16-pair tile) work item per workgroup; each wave owns
-// 16 rows and runs its K loop on its own (no LDS, no barriers), one step of
-// operands loaded ahead of the MFMAs that use the current one. The 4 waves read
-// the same B bytes, which L1/L2 serve after the first.
 template <bool GATEUP>
-__global__ __launch_bounds__(256, GATEUP ? 2 : 3) void k_grouped_gemm(GroupedArgs a) {
+__global__ __launch_bounds__(512, 2) void k_grouped_gemm(GroupedArgs a) {
+  __shared__ __align__(16) uint8_t bst[2][kBStage];
+  __shared__ __align__(16) uint32_t bsc[2][kPairTile * 4];
+  __shared__ __align__(16) uint8_t ast[kGemmWaves][2][kAStage];
+  __shared__ __align__(16) uint8_t zero[32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, g = lane >> 4, t = i & 3;
+  constexpr int NM = GATEUP ? 2 : 1;
+  constexpr int kRows = 16 * kGemmWaves / NM;  // rows per work item
   // Work items are ordered (expert, row tile, pair tile of the expert), and each
   // XCD (workgroups are dispatched round-robin over kXcds) takes one contiguous
   // range of them: the items that share an expert's row tile (A) or its pairs'
   // images (B) run on the same XCD and meet in its L2.
-  const int n_rt = (a.M + kRowTile - 1) / kRowTile;
+  const int n_rt = (a.M + kRows - 1) / kRows;
   const int n_work = n_rt * a.tile_off[a.E];
   const int per_xcd = (n_work + kXcds - 1) / kXcds;
   const int loc = blockIdx.x / kXcds;
@@ -173,70 +162,132 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void k_grouped_gemm(GroupedArg
   const int rt = wl / nt_e, tl = wl - rt * nt_e;
   const int p0 = a.exp_off[e] + tl * kPairTile;
   const int np = min(kPairTile, a.exp_off[e + 1] - p0);
-  const int row0 = rt * kRowTile + wave * 16;
-  if (row0 >= a.M) return;  // uniform per wave; no barriers follow
+  if (tid < 8) reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
 
   const int nbK = a.K >> 5, S = (nbK + 3) >> 2;
-  const int row = min(row0 + i, a.M - 1);
   const uint64_t rb = (uint64_t)nbK * 17;
-  constexpr int NM = GATEUP ? 2 : 1;
-  const uint8_t* wrow[NM];
-  wrow[0] = a.w0 + a.off0[e] + (uint64_t)row * rb;
-  if (GATEUP) wrow[NM - 1] = a.w1 + a.off1[e] + (uint64_t)row * rb;
-  uint32_t sh[NM];
+  const int m = GATEUP ? (wave >> 2) : 0;
+  const int row0 = rt * kRows + (GATEUP ? (wave & 3) : wave) * 16;
+  const bool rows_in = row0 < a.M;          // wave-uniform; other waves still load B and sync
+  const int row0c = min(row0, a.M - 16);    // M is a multiple of 16
+  const uint8_t* W = (m ? a.w1 + a.off1[e] : a.w0 + a.off0[e]) + (uint64_t)row0c * rb;
+  // this thread's B pieces (q = j*512 + tid): pair q/32, block (q/8)%4, part q%8
+  const uint8_t* bsrc[2];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) sh[m] = (uint32_t)reinterpret_cast<uintptr_t>(wrow[m]) & 3u;
-  const uint8_t* bsrc[4];
-  const uint32_t* bsc[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int p = p0 + min(4 * c + (i >> 2), np - 1);
+  for (int j = 0; j < 2; ++j) {
+    const int q = j * 512 + tid;
+    const int p = p0 + min(q >> 5, np - 1);
     const int r = a.pair_tok ? a.pair_tok[p] : p;
-    bsrc[c] = a.img + (size_t)r * nbK * kImgBytes + t * 32 + 16 * (g & 1);
-    bsc[c] = a.isc + (size_t)r * nbK;
+    bsrc[j] = a.img + (size_t)r * nbK * kImgBytes + (q & 7) * 16;
   }
-  f32x4 acc[NM][4];
+  const int sq = tid & 127;  // scale word sq (waves 0-1): pair sq/4, block sq%4
+  const uint32_t* ssrc;
+  {
+    const int p = p0 + min(sq >> 2, np - 1);
+    const int r = a.pair_tok ? a.pair_tok[p] : p;
+    ssrc = a.isc + (size_t)r * nbK;
+  }
+  // A pieces of this wave (p = it*64 + lane): row p/6, piece p%6 (p >= 96: pad)
+  const uint8_t* arow[2];
+  int apc[2];
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[m][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < 2; ++it) {
+    const int pp = it * 64 + lane;
+    const int r = min(pp / kAPieces, 15);
+    apc[it] = min(pp - r * kAPieces, kAPieces - 1);
+    arow[it] = W + (uint64_t)r * rb;
+  }
+  const uintptr_t my_row = reinterpret_cast<uintptr_t>(W + (uint64_t)i * rb);
 
-  StepOps<NM> ops[2];
-  load_step<NM>(ops[0], 0, nbK, g, t, wrow, bsrc, bsc);
+  auto issue = [&](int st, int buf) {
 #pragma unroll
-  for (int st = 0; st < kMaxSteps; ++st) {
-    if (st < S) {
-      if (st + 1 < S) load_step<NM>(ops[(st + 1) & 1], st + 1, nbK, g, t, wrow, bsrc, bsc);
-      const StepOps<NM>& o = ops[st & 1];
-      const int cb = 4 * st + g;  // this lane's A block
+    for (int it = 0; it < 2; ++it) {
+      const uintptr_t first = reinterpret_cast<uintptr_t>(arow[it] + (size_t)(4 * st) * 17) & ~(uintptr_t)15;
+      const uintptr_t last = (reinterpret_cast<uintptr_t>(arow[it] + (size_t)nbK * 17) - 1) & ~(uintptr_t)15;
+      const uintptr_t src = min(first + 16 * (uintptr_t)apc[it], last);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), &ast[wave][buf][it * 1024], 16, 0, 0);
+    }
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const uint32_t shb = (sh[m] + (uint32_t)min(cb, nbK - 1)) & 3u;
+    for (int j = 0; j < 2; ++j) {
+      const int q = j * 512 + tid;
+      const int blk = min(4 * st + ((q >> 3) & 3), nbK - 1);
+      __builtin_amdgcn_global_load_lds(bsrc[j] + (size_t)blk * kImgBytes, &bst[buf][(j * 512 + wave * 64) * 16], 16,
+                                       0, 0);
+    }
+    if (wave < 2)
+      __builtin_amdgcn_global_load_lds(ssrc + min(4 * st + (sq & 3), nbK - 1), &bsc[buf][wave * 64], 4, 0, 0);
+  };
+
+  f32x4 acc[8];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[m][c] = mfma_raw(o.a[m], shb, cb < nbK, o.b[c], o.sb[c], acc[m][c]);
+  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  issue(0, 0);
+  for (int st = 0; st < S; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < S) {
+      __syncthreads();  // every wave is done with buffer buf^1 (step st-1)
+      issue(st + 1, buf ^ 1);
+      if (wave < 2)
+        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // step st's loads have landed
+      else
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    } else {
+      vm_drain();
+    }
+    __syncthreads();  // step st's A and B are in LDS for every wave
+    if (rows_in) {
+      const int b = 4 * st + g;  // this lane's A block
+      const int lead = (int)((my_row + (uintptr_t)(4 * st) * 17) & 15u);
+      const int off = i * (kAPieces * 16) + lead + g * 17;
+      const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][buf][off & ~3]);
+      RawBlk ra;
+      ra.d[0] = wp[0], ra.d[1] = wp[1], ra.d[2] = wp[2], ra.d[3] = wp[3], ra.d[4] = wp[4];
+      const int b0 = 4 * st + (g >> 1), b1 = b0 + 2;
+      const int sb_off = (b < nbK ? g : 0);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int pr = 4 * c + (i >> 2);
+        const uint8_t* pb = &bst[buf][pr * 4 * kImgBytes + t * 32 + 16 * (g & 1)];
+        const i32x4 v0 = *reinterpret_cast<const i32x4*>(b0 < nbK ? pb + (g >> 1) * kImgBytes : zero);
+        const i32x4 v1 = *reinterpret_cast<const i32x4*>(b1 < nbK ? pb + (2 + (g >> 1)) * kImgBytes : zero);
+        const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        const int sb = (int)((bsc[buf][pr * 4 + sb_off] >> (8 * t)) & 0xFFu);
+        acc[c] = mfma_raw(ra, (uint32_t)off & 3u, b < nbK, B, sb, acc[c]);
       }
     }
   }
   // epilogue: columns 4*tl .. 4*tl+3 of group c are the 4 terms of pair 4c+tl
+  float* xch = reinterpret_cast<float*>(&bst[0][0]);  // gate results for the up waves (32 KB)
+  if (GATEUP) {
+    __syncthreads();  // the K loop's LDS is no longer read
+    if (m == 0) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xch[(((wave & 3) * 8 + c) * 4 + r) * 64 + lane] = sum4(acc[c][r]);
+    }
+    __syncthreads();
+    if (m == 0) return;
+  }
+  if (!rows_in) return;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float v0 = sum4(acc[0][c][r]);
-      const float v1 = GATEUP ? sum4(acc[NM - 1][c][r]) : 0.f;
+      const float v = sum4(acc[c][r]);
       const int pl = 4 * c + (i >> 2);
       const int orow = row0 + 4 * g + r;
       if (t == 0 && pl < np && orow < a.M) {
         const int p = p0 + pl;
         float o;
         if (GATEUP) {
-          float gv = v0, uv = v1;
+          float gv = xch[(((wave & 3) * 8 + c) * 4 + r) * 64 + lane], uv = v;
           if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
           if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
           const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
           o = h * a.pair_w[p];
         } else {
-          o = v0;
+          o = v;
         }
         a.out[(size_t)p * a.M + orow] = o;
       }
@@ -351,8 +402,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   {
     ProfScope ps(K, "grouped_gateup");
-    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + kRowTile - 1) / kRowTile) * max_tiles)),
-                       dim3(256), 0, K.s, a);
+    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + 63) / 64) * max_tiles)), dim3(512), 0, K.s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
@@ -369,8 +419,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   d.M = H, d.K = I, d.E = E, d.max_tiles = max_tiles;
   {
     ProfScope ps(K, "grouped_down");
-    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3((unsigned)(((H + kRowTile - 1) / kRowTile) * max_tiles)),
-                       dim3(256), 0, K.s, d);
+    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3((unsigned)(((H + 127) / 128) * max_tiles)), dim3(512), 0, K.s, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
