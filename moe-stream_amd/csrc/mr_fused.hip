@@ -210,6 +210,101 @@ __device__ __forceinline__ f32x4 stream_chain(const uint8_t* W, uint64_t rb, int
   return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
 }
 
+// The same chunk stream with the chunks held in VGPRs while they are in flight: kChunkAhead
+// chunks beyond the one being multiplied are requested (16 VGPRs each), so a wave keeps
+// (kChunkAhead + 1) x 4 KB of loads outstanding instead of the one chunk two LDS buffers
+// allow. A landed chunk is written to this wave's LDS buffer (same layout as stream_issue
+// produces) and the MFMA windows are read back from there. The code is straight-line over
+// kMaxChunks chunks: chunks past the row end load clamped pieces and multiply the zero B
+// line, so the compiler's own vmcnt waits stay exact.
+#ifndef MR_CHUNK_AHEAD
+#define MR_CHUNK_AHEAD 2
+#endif
+constexpr int kChunkAhead = MR_CHUNK_AHEAD;
+
+// Per-lane piece geometry of a 16-row tile, as byte offsets from the tile's first row (W):
+// lane piece q = it*64 + lane is piece pc of row `row`; rowa = (W & 15) + row*rb is the row's
+// start counted from the 16-byte boundary at or below W, and lastr its last piece.
+struct PieceMap {
+  uint32_t rowa[kStageLoads], pc16[kStageLoads], lastr[kStageLoads];
+};
+__device__ __forceinline__ PieceMap piece_map(const uint8_t* W, uint32_t rb, int nb, int lane) {
+  PieceMap m;
+  const uint32_t a = (uint32_t)(reinterpret_cast<uintptr_t>(W) & 15u);
+#pragma unroll
+  for (int it = 0; it < kStageLoads; ++it) {
+    const int q = it * 64 + lane;
+    const int row = min(q / kRowPieces, 15);
+    const int pc = min(q - row * kRowPieces, kRowPieces - 1);
+    m.rowa[it] = a + (uint32_t)row * rb;
+    m.pc16[it] = 16u * (uint32_t)pc;
+    m.lastr[it] = (m.rowa[it] + (uint32_t)nb * 17u - 1u) & ~15u;
+  }
+  return m;
+}
+// Chunk c of the tile into v (this lane's 4 pieces). Wa = W rounded down to 16 bytes (uniform).
+__device__ __forceinline__ void piece_fetch(const uint8_t* Wa, const PieceMap& m, int c, i32x4 (&v)[kStageLoads]) {
+  const uint32_t cb = 17u * 4u * kStreamSteps * (uint32_t)c;
+#pragma unroll
+  for (int it = 0; it < kStageLoads; ++it) {
+    const uint32_t first = min((m.rowa[it] + cb) & ~15u, m.lastr[it]);
+    const uint32_t off = min(first + m.pc16[it], m.lastr[it]);  // never past the row's last piece
+    v[it] = *(const __attribute__((address_space(1))) i32x4*)(Wa + off);  // global, not flat
+  }
+}
+
+__device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, int nb, uint8_t* stage,
+                                                const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
+                                                int lane, int i, int g) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd steps
+  const uint8_t* Wa = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(W) & ~(uintptr_t)15);
+  const PieceMap m = piece_map(W, rb, nb, lane);
+  const uint32_t rowa_i = (uint32_t)(reinterpret_cast<uintptr_t>(W) & 15u) + (uint32_t)i * rb;  // this lane's row
+  const uint32_t last_i = rowa_i + (uint32_t)(nb - 1) * 17u;
+  const int nc = (nb + 4 * kStreamSteps - 1) / (4 * kStreamSteps);  // chunks in this row
+  i32x4 v[kMaxChunks][kStageLoads];
+#pragma unroll
+  for (int c = 0; c < kChunkAhead && c < kMaxChunks; ++c) piece_fetch(Wa, m, c, v[c]);
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    // The branch on c < nc (wave-uniform) also closes a basic block per chunk, which keeps
+    // the chunk's MFMAs from being scheduled after later chunks' operand loads.
+    if (c >= nc) break;
+    // Fetches are unconditional (chunks past the row load clamped pieces), so the loads issued
+    // after chunk c are the same on every path and its wait is exact.
+    if (c + kChunkAhead < kMaxChunks) piece_fetch(Wa, m, c + kChunkAhead, v[c + kChunkAhead]);
+    uint8_t* buf = stage + (c & 1) * kStageBytes;
+#pragma unroll
+    for (int it = 0; it < kStageLoads; ++it) *reinterpret_cast<i32x4*>(buf + it * 1024 + lane * 16) = v[c][it];
+    __builtin_amdgcn_wave_barrier();
+    const int b0 = 4 * kStreamSteps * c;
+    const int lead = (int)(min(rowa_i + (uint32_t)b0 * 17u, last_i) & 15u);  // chunk start within its first piece
+    RawBlk r[kStreamSteps];
+    i32x8 B[kStreamSteps];
+    int sb[kStreamSteps], off[kStreamSteps];
+#pragma unroll
+    for (int s = 0; s < kStreamSteps; ++s) {  // every operand of the chunk is loaded first
+      const int st = kStreamSteps * c + s;
+      const int b = 4 * st + g;
+      off[s] = i * (kRowPieces * 16) + lead + (b - b0) * 17;  // <= i*240 + 202: inside the row slot
+      const uint32_t* wp = reinterpret_cast<const uint32_t*>(buf + (off[s] & ~3));
+      r[s].d[0] = wp[0], r[s].d[1] = wp[1], r[s].d[2] = wp[2], r[s].d[3] = wp[3], r[s].d[4] = wp[4];
+      load_b(img, sc, zero, st, nb, i, g, B[s], sb[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < kStreamSteps; ++s) {
+      const int st = kStreamSteps * c + s;
+      const int b = 4 * st + g;
+      if (st & 1)
+        acc1 = mfma_raw_nb(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc1);
+      else
+        acc = mfma_raw_nb(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   extern __shared__ __align__(16) uint8_t lds_dyn[];
@@ -237,6 +332,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     const int e = bid * 4 + wave;
     if (e < a.E) {
       const float* w = a.router_w + (size_t)e * a.H;
+      // bias and mask are loaded with the rows, not after the reduction (an HBM round trip)
+      const float rbias = a.router_b ? a.router_b[e] : 0.f;
+      const float rmask = a.mask ? a.mask[e] : 0.f;
       f32x4 xv[kRouterVec], wv[kRouterVec];  // every load issued before the first use
 #pragma unroll
       for (int j = 0; j < kRouterVec; ++j) {
@@ -255,8 +353,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       }
       acc = wave_sum(acc);
       if (lane == 0) {
-        if (a.router_b) acc = acc + a.router_b[e];
-        if (a.mask) acc = acc + a.mask[e];
+        if (a.router_b) acc = acc + rbias;
+        if (a.mask) acc = acc + rmask;
         st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
         vm_drain();  // the logit is stored before the barrier that precedes its count
       }
@@ -310,8 +408,21 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const int S = (nbH + 3) >> 2;
       const uint64_t rb = (uint64_t)nbH * 17;
       const uint8_t* W = (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]) + (uint64_t)(pair * 32 + tile * 16) * rb;
+      // the epilogue's biases (wave 0, lanes < 32), loaded before the weight stream
+      float gbias = 0.f, ubias = 0.f;
+      if (wave == 0 && lane < 32) {
+        const size_t bi = (size_t)e * a.I + pair * 32 + lane;
+        if (a.gate_b) gbias = a.gate_b[bi];
+        if (a.up_b) ubias = a.up_b[bi];
+      }
+#if MR_CHUNK_AHEAD > 0
+      (void)S;
+      f32x4 dacc = stream_chain_v(W, (uint32_t)rb, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
+                                  lds_zero, lane, i, g);
+#else
       f32x4 dacc = stream_chain(W, rb, S, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
                                 lds_zero, lane, i, g);
+#endif
       TRACE(3);
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
@@ -325,9 +436,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           const int t2 = lane >> 4, r16 = lane & 15;
           float gv = lds_part[(0 * 2 + t2) * 16 + r16];
           float uv = lds_part[(1 * 2 + t2) * 16 + r16];
-          const int rr = pair * 32 + lane;
-          if (a.gate_b) gv = gv + a.gate_b[(size_t)e * a.I + rr];
-          if (a.up_b) uv = uv + a.up_b[(size_t)e * a.I + rr];
+          if (a.gate_b) gv = gv + gbias;
+          if (a.up_b) uv = uv + ubias;
           const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
           lds_act[lane] = h * wsl;
         }

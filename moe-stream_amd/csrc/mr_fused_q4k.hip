@@ -260,6 +260,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     const int e = bid * 4 + wave;
     if (e < a.E + a.has_sh) {
       const float* w = e < a.E ? a.router_w + (size_t)e * a.H : a.sh_gate_inp;
+      // bias and mask are loaded with the rows, not after the reduction (an HBM round trip)
+      const float rbias = (e < a.E && a.router_b) ? a.router_b[e] : 0.f;
+      const float rmask = (e < a.E && a.mask) ? a.mask[e] : 0.f;
       f32x4 xv[kQ4RouterVec], wv[kQ4RouterVec];
 #pragma unroll
       for (int j = 0; j < kQ4RouterVec; ++j) {
@@ -279,8 +282,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       acc = wave_sum(acc);
       if (lane == 0) {
         if (e < a.E) {
-          if (a.router_b) acc = acc + a.router_b[e];
-          if (a.mask) acc = acc + a.mask[e];
+          if (a.router_b) acc = acc + rbias;
+          if (a.mask) acc = acc + rmask;
         }
         st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
         vm_drain();  // the logit is stored before the barrier that precedes its count
@@ -339,6 +342,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const size_t rb = (size_t)nsbH * 144;
       uint4 ch[1][kQ4GuIt];
       region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
+      // the epilogue's biases (wave 0, lanes < 16), loaded before the dot products
+      float gbias = 0.f, ubias = 0.f;
+      if (wave == 0 && lane < 16 && !sh) {
+        const size_t bi = (size_t)e * a.I + urow * 16 + lane;
+        if (a.gate_b) gbias = a.gate_b[bi];
+        if (a.up_b) ubias = a.up_b[bi];
+      }
       float* hdec = reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16;
       region_headers<kQ4GuIt, 1>(ch, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
       XTRACE(wave);  // per wave: weights landed, headers decoded
@@ -353,8 +363,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       if (wave == 0 && lane < 16) {
         const int rr = urow * 16 + lane;
         float g = gu_part[0][lane], u = gu_part[1][lane];
-        if (!sh && a.gate_b) g = g + a.gate_b[(size_t)e * a.I + rr];
-        if (!sh && a.up_b) u = u + a.up_b[(size_t)e * a.I + rr];
+        if (!sh && a.gate_b) g = g + gbias;
+        if (!sh && a.up_b) u = u + ubias;
         const float hact = (!sh && a.act == MR_ACT_SWIGLU_OAI) ? swiglu_oai(g, u, a.alpha, a.limit) : silu_mul(g, u);
         const float h = hact * sel_w[slot];
         float m = max8(fabsf(h));

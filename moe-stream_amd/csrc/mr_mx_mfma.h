@@ -136,6 +136,21 @@ __device__ __forceinline__ f32x4 mfma_raw(const RawBlk& r, uint32_t sh, bool val
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
 }
 
+// mfma_raw without a branch: each code dword is the 64-bit dword pair shifted right by
+// sh+1 bytes (a shift of 4 bytes selects the upper dword). For chains whose windows are read
+// just before use, where a divergent branch around the shifts would cost more than the shifts.
+__device__ __forceinline__ f32x4 mfma_raw_nb(const RawBlk& r, uint32_t sh, bool valid, const i32x8& B,
+                                             int sb, f32x4 acc) {
+  const uint32_t t8 = 8u * (sh + 1u);
+  const uint32_t q0 = (uint32_t)((((uint64_t)r.d[1] << 32) | r.d[0]) >> t8);
+  const uint32_t q1 = (uint32_t)((((uint64_t)r.d[2] << 32) | r.d[1]) >> t8);
+  const uint32_t q2 = (uint32_t)((((uint64_t)r.d[3] << 32) | r.d[2]) >> t8);
+  const uint32_t q3 = (uint32_t)((((uint64_t)r.d[4] << 32) | r.d[3]) >> t8);
+  const int sa = valid ? (int)((r.d[0] >> (8u * sh)) & 0xFFu) : 127;
+  const i32x8 A = {(int)q0, (int)q1, (int)q2, (int)q3, 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
+}
+
 // B operand for a prepared-A chain: column i reads term i%4 (columns 4..15 repeat
 // the terms; only columns 0..3 are summed afterwards, and the data is finite), block
 // indices clamp to the last block (the A operand of an invalid block is zero).
