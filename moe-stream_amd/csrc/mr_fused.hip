@@ -21,8 +21,8 @@
 //   D:       D[4g + r][i] in element r.
 //
 // Three groups of workgroups share one grid:
-//   [0, R)        router: one expert logit per wave; publishes the logit and
-//                 bumps a counter.
+//   [0, R)        router: one expert logit per wave; publishes it as a flagged
+//                 64-bit word (logit bits, launch number + 1).
 //   [R, R+ND)     down: 16 output rows; wave w takes routed slot w (top_k <= 4).
 //                 Its down weights are loaded into registers before the gate/up
 //                 results exist, so their HBM traffic overlaps the gate/up phase.
@@ -31,15 +31,16 @@
 //                 split is built in LDS while the router runs. Epilogue: bias,
 //                 SwiGLU, x routing weight, split into the down B image.
 // Workgroups are dispatched in index order; fused_supported keeps R + ND below
-// the CU count and the whole grid within 3 workgroups per CU (143 VGPRs, about
+// the CU count and the whole grid within 3 workgroups per CU (159 VGPRs, about
 // 50 KB LDS each), so every workgroup is resident from the start and no wait
 // can depend on a workgroup that has not been dispatched.
-// Small cross-workgroup values (logits, counters, the down B image) are written
-// with agent-coherent stores ordered by s_waitcnt; the down workgroups read the
-// image through L2 after one agent-scope acquire. Every wait is bounded (the
-// context's spin limit); a wait that runs out sets an error word read at
-// mr_sync and the launch still exits. The last workgroup to finish resets the
-// counters for the next launch.
+// Cross-workgroup values are written with agent-scope stores: the logits carry
+// their launch flag in the same 64-bit store, so routing polls them directly; the
+// down B image is announced by a monotonic counter (64 copies) bumped after the
+// image stores have completed. Each workgroup keeps its own launch number (read at
+// entry, stored +1 at exit), so nothing is reset between launches. Every wait is
+// bounded (the context's spin limit); a wait that runs out sets an error word read
+// at mr_sync and the launch still exits.
 #include "mr_device.h"
 #include "mr_internal.h"
 #include "mr_fused_common.h"
@@ -351,16 +352,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
         acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
       }
-      acc = wave_sum(acc);
-      if (lane == 0) {
-        if (a.router_b) acc = acc + rbias;
-        if (a.mask) acc = acc + rmask;
-        st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
-        vm_drain();  // the logit is stored before the barrier that precedes its count
-      }
+      acc = wave_sum(acc);  // the same bits in every lane (butterfly of commutative adds)
+      if (a.router_b) acc = acc + rbias;
+      if (a.mask) acc = acc + rmask;
+      put_logit(a.fs, (uint32_t)a.E, e, seq, acc);
     }
-    __syncthreads();
-    if (tid == 0) count(a.fs + FS_ROUTE, bid, (uint32_t)min(4, a.E - bid * 4));  // this workgroup's logits
     TRACE(1);
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up

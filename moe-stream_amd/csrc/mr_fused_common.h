@@ -21,15 +21,16 @@ namespace mr {
 
 constexpr int kCopies = 64;     // copies of each producer counter, one 128-byte line apart
 constexpr int kCopyStride = 32;  // words
-enum : int {
-  FS_ROUTE = 0,                                // [kCopies] counter: logits published
-  FS_GU = FS_ROUTE + kCopies * kCopyStride,    // [kCopies] counter: gate/up units finished
-  FS_LOGITS = FS_GU + kCopies * kCopyStride,   // logits of the current launch (E experts, then extras)
-  FS_WGSEQ = FS_LOGITS + 1024                  // [grid] launches completed, one word per workgroup
-};
 constexpr int kMaxLogits = 1024;
 constexpr int kMaxGrid = 1024;
-constexpr int kLayerSyncWords = FS_WGSEQ + kMaxGrid;
+constexpr int kLogitCopies = 32;  // copies of the published logits (consumers spread their polls)
+enum : int {
+  FS_GU = 0,                                   // [kCopies] counter: gate/up units finished
+  FS_WGSEQ = FS_GU + kCopies * kCopyStride,    // [grid] launches completed, one word per workgroup
+  FS_LOGITS = FS_WGSEQ + kMaxGrid              // [kLogitCopies][n_logits] (logit bits, launch flag)
+                                               // word pairs: E experts, then extras
+};
+constexpr int kLayerSyncWords = FS_LOGITS + kLogitCopies * 2 * kMaxLogits;
 
 // Launch sequence number of this layer's kernel. Every launch of a layer runs
 // the same grid, so each workgroup keeps its own count (read at entry, stored
@@ -147,6 +148,32 @@ __device__ __forceinline__ void st_sc1(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ uint32_t add_sc1(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint64_t ld64_sc1(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Published logits: kLogitCopies copies of n_logits 64-bit words (logit bits, seq + 1),
+// each copy starting on a 128-byte line. A reader that sees the flag half sees the value
+// half (aligned 8-byte stores are single-copy atomic), so no counter or store drain is
+// needed; the flag of the previous launch is seq, never seq + 1, and the block starts
+// zeroed (flag 0). Consumer workgroups poll copy (blockIdx % kLogitCopies), which
+// spreads their polls over many lines instead of one.
+__device__ __forceinline__ uint64_t* logit_copy(const uint32_t* fs, uint32_t n_logits, int copy) {
+  const uint32_t stride = (2u * n_logits + 31u) & ~31u;  // words
+  return reinterpret_cast<uint64_t*>(const_cast<uint32_t*>(fs) + FS_LOGITS + (size_t)copy * stride);
+}
+// Lane c < kLogitCopies of a wave stores copy c of logit e (v is wave-uniform).
+__device__ __forceinline__ void put_logit(uint32_t* fs, uint32_t n_logits, int e, uint32_t seq, float v) {
+  const int lane = threadIdx.x & 63;
+  if (lane < kLogitCopies) {
+    const uint64_t w = ((uint64_t)(seq + 1u) << 32) | (uint64_t)__float_as_uint(v);
+    __hip_atomic_store(logit_copy(fs, n_logits, lane) + e, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+// Logit e of the current launch; valid once route_wave has returned true in this wave.
+__device__ __forceinline__ float get_logit(const uint32_t* fs, uint32_t n_logits, int e) {
+  const uint64_t* p = logit_copy(fs, n_logits, (int)(blockIdx.x % kLogitCopies)) + e;
+  return __uint_as_float(ld_sc1(reinterpret_cast<const uint32_t*>(p)));
+}
 // All vector memory operations this wave has issued have completed.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // All LDS operations this wave has issued have completed.
@@ -211,15 +238,31 @@ __device__ __forceinline__ void cas_desc(uint32_t& ka, int& ia, uint32_t& kb, in
 __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, float* sel_w, int* ord) {
   const int lane = threadIdx.x & 63;
   RTRACE(0);
-  if (!wait_count(rc.fs + FS_ROUTE, (seq + 1u) * rc.n_logits, rc.spin_limit)) return false;
-  RTRACE(1);
   const int nj = (rc.E + 63) >> 6;  // values per lane (wave-uniform)
+  // Poll the flagged logit words until every entry (experts and extras) carries this
+  // launch's flag; the values come with the flags, in the same loads.
+  const uint64_t* lw = logit_copy(rc.fs, rc.n_logits, (int)(blockIdx.x % kLogitCopies));
+  const uint32_t flag = seq + 1u;
+  const int ex = lane < (int)rc.n_logits - rc.E ? rc.E + lane : -1;  // an extra entry of this lane
   float v[kRouteVals];
+  for (uint32_t it = 0;; ++it) {
+    bool ok = true;
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = (j < nj && e < rc.E) ? __uint_as_float(ld_sc1(rc.fs + FS_LOGITS + e)) : -INFINITY;
+    for (int j = 0; j < kRouteVals; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = -INFINITY;
+      if (j < nj && e < rc.E) {
+        const uint64_t w = ld64_sc1(lw + e);
+        v[j] = __uint_as_float((uint32_t)w);
+        ok = ok && (uint32_t)(w >> 32) == flag;
+      }
+    }
+    if (ex >= 0) ok = ok && (uint32_t)(ld64_sc1(lw + ex) >> 32) == flag;
+    if (__ballot(!ok) == 0ull) break;
+    if (it >= rc.spin_limit) return false;
+    __builtin_amdgcn_s_sleep(2);
   }
+  RTRACE(1);
   // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen
   // mode; exp is monotonic, so the order differs only where two logits round to the
   // same probability (a tie by value, which the tests treat as ambiguous).

@@ -279,18 +279,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
         acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
       }
-      acc = wave_sum(acc);
-      if (lane == 0) {
-        if (e < a.E) {
-          if (a.router_b) acc = acc + rbias;
-          if (a.mask) acc = acc + rmask;
-        }
-        st_sc1(a.fs + FS_LOGITS + e, __float_as_uint(acc));
-        vm_drain();  // the logit is stored before the barrier that precedes its count
+      acc = wave_sum(acc);  // the same bits in every lane (butterfly of commutative adds)
+      if (e < a.E) {
+        if (a.router_b) acc = acc + rbias;
+        if (a.mask) acc = acc + rmask;
       }
+      put_logit(a.fs, (uint32_t)(a.E + a.has_sh), e, seq, acc);
     }
-    __syncthreads();
-    if (tid == 0) count(a.fs + FS_ROUTE, bid, (uint32_t)min(4, a.E + a.has_sh - bid * 4));  // this workgroup's logits
     TRACE(1);
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
@@ -327,7 +322,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       if (!route_wave(rc, seq, sel_i, sel_w, sel_o)) {
         if (lane == 0) ok_flag = 0, fail(a.err);
       } else if (a.has_sh && lane == 0) {
-        const float z = __uint_as_float(ld_sc1(a.fs + FS_LOGITS + a.E));
+        const float z = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
         sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(z) : 1.f;
       }
     }
