@@ -84,30 +84,67 @@ struct FusedArgs {
   unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][16] timestamps
 };
 
-// D += sum over the K steps of one 16-row tile: A from raw windows `rw`, B from
-// a B image in LDS.
-__device__ __forceinline__ f32x4 mfma_chain(const RawBlk (&rw)[kSteps], uint32_t sh, int S, int nb,
-                                            const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
-                                            int i, int g, f32x4 acc) {
-  // Every one of the kSteps steps is issued, with no branch between them, so the LDS
-  // operand loads of later steps can be scheduled ahead: steps at or past S read the
-  // zero B line (and issue_rows zeroed their A), so they add exactly 0.
-  // Step j+1's B operand is loaded before step j's MFMA is issued.
-  (void)S;
-  f32x4 acc1 = {0.f, 0.f, 0.f, 0.f};  // odd steps: two independent MFMA dependency chains
-  i32x8 Bn;
-  int sbn;
-  load_b(img, sc, zero, 0, nb, i, g, Bn, sbn);
+// In place, raw windows -> MFMA A operands: d[0..3] = the 16 code bytes, d[4] = the e8m0
+// scale byte. The window of block c = 4j+g starts (sh + c) & 3 = (sh + g) & 3 bytes before
+// the block (17 = 1 mod 4), so the byte shift is the same for every step of a lane. Blocks
+// past the row end (clamped to the last block, or zero windows) meet an all-zero B operand,
+// so any finite operand serves them: their codes are finite whatever the bytes, but their
+// scale byte is set to 127, since a misaligned byte could be 0xFF (NaN, and NaN * 0 = NaN).
+// Done while the workgroup waits for the gate/up results.
+__device__ __forceinline__ void prep_rows(RawBlk (&rw)[kSteps], uint32_t sh, int nb, int g) {
+  const uint32_t s0 = (sh + (uint32_t)g) & 3u;  // scale byte position
+  const uint32_t t = s0 + 1u;                   // code bytes start
+  const bool hi = t == 4u;
 #pragma unroll
   for (int j = 0; j < kSteps; ++j) {
-    const i32x8 B = Bn;
-    const int sb = sbn;
-    if (j + 1 < kSteps) load_b(img, sc, zero, j + 1, nb, i, g, Bn, sbn);
-    const int c = 4 * j + g;
+    RawBlk& r = rw[j];
+    const uint32_t sa = 4 * j + g < nb ? (r.d[0] >> (8u * s0)) & 0xFFu : 127u;
+    const uint32_t q0 = hi ? r.d[1] : __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
+    const uint32_t q1 = hi ? r.d[2] : __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
+    const uint32_t q2 = hi ? r.d[3] : __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
+    const uint32_t q3 = hi ? r.d[4] : __builtin_amdgcn_alignbyte(r.d[4], r.d[3], t);
+    r.d[0] = q0, r.d[1] = q1, r.d[2] = q2, r.d[3] = q3, r.d[4] = sa;
+  }
+}
+
+// D of one 16-row tile from prepared A operands (prep_rows) and a B image in LDS whose
+// blocks from nb up to 4*kSteps-1 and their scale words are zero. Lane (i, g) reads term i&3 (columns
+// 4..15 repeat columns 0..3; only columns 0..3 are summed) at fixed offsets from one base:
+// block 4j + (g>>1) of step j is at j*512, the block two later at j*512 + 256, and the
+// scale byte of block 4j+g at j*16 -- no address arithmetic per step.
+__device__ __forceinline__ f32x4 mfma_chain_p(const RawBlk (&rw)[kSteps], const uint8_t* img,
+                                              const uint32_t* sc, int i, int g) {
+  const uint8_t* bb = img + (g >> 1) * kImgBytes + (i & 3) * 32 + 16 * (g & 1);
+  const uint8_t* sbp = reinterpret_cast<const uint8_t*>(sc) + g * 4 + (i & 3);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  // B operands (and scale bytes) of steps j+1 and j+2 are in flight while step j multiplies
+  constexpr int kAhead = 2;
+  i32x4 b0[kAhead + 1], b1[kAhead + 1];
+  int sb[kAhead + 1];
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) {
+    b0[j] = *reinterpret_cast<const i32x4*>(bb + j * 4 * kImgBytes);
+    b1[j] = *reinterpret_cast<const i32x4*>(bb + j * 4 * kImgBytes + 2 * kImgBytes);
+    sb[j] = sbp[j * 16];
+  }
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) {
+    const int cur = j % (kAhead + 1);
+    if (j + kAhead < kSteps) {
+      const int nx = (j + kAhead) % (kAhead + 1);
+      b0[nx] = *reinterpret_cast<const i32x4*>(bb + (j + kAhead) * 4 * kImgBytes);
+      b1[nx] = *reinterpret_cast<const i32x4*>(bb + (j + kAhead) * 4 * kImgBytes + 2 * kImgBytes);
+      sb[nx] = sbp[(j + kAhead) * 16];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the loads above stay ahead of this step's MFMA
+    const i32x8 B = {b0[cur][0], b0[cur][1], b0[cur][2], b0[cur][3], b1[cur][0], b1[cur][1], b1[cur][2], b1[cur][3]};
+    const RawBlk& r = rw[j];
+    const i32x8 A = {(int)r.d[0], (int)r.d[1], (int)r.d[2], (int)r.d[3], 0, 0, 0, 0};
     if (j & 1)
-      acc1 = mfma_raw(rw[j], (sh + (uint32_t)min(c, nb - 1)) & 3u, c < nb, B, sb, acc1);
+      acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc1, 4, 0, 0, (int)r.d[4], 0, sb[cur]);
     else
-      acc = mfma_raw(rw[j], (sh + (uint32_t)min(c, nb - 1)) & 3u, c < nb, B, sb, acc);
+      acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, (int)r.d[4], 0, sb[cur]);
+    __builtin_amdgcn_sched_barrier(0);
   }
   return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
 }
@@ -143,6 +180,7 @@ constexpr int kMaxChunks = (kSteps + kStreamSteps - 1) / kStreamSteps;
 static_assert(16 * kRowPieces <= kStageLoads * 64, "a chunk's pieces fit one buffer");
 static_assert(15 + 17 * 4 * kStreamSteps + 3 <= 16 * kRowPieces, "a row slot holds the chunk and its window tail");
 static_assert(kStageOff + 4 * 2 * kStageBytes <= 4 * kImgVec * 1024, "stage buffers fit the dynamic LDS");
+static_assert(4 * kSteps * kImgBytes <= kImgVec * 1024 && 4 * kSteps <= 128, "a down slot image holds 4*kSteps blocks");
 
 __device__ __forceinline__ void stream_issue(const uint8_t* W, uint64_t rb, int nb, int c, uint8_t* buf,
                                              int lane) {
@@ -478,6 +516,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
+      if (slot < a.k) prep_rows(rd, sh, nbI, g);  // waits for the weights: they land long before gate/up ends
       TRACE(2);
       if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
@@ -502,11 +541,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
             if (lane < nbI) wsc[lane] = sc0;
             if (lane + 64 < nbI) wsc[lane + 64] = sc1v;
             vm_drain();  // the slot image has landed in LDS
+            // blocks nbI .. 4*kSteps-1 (read by the last steps, which have all-zero A) and
+            // their scale words are zero; after the drain: the last direct load also wrote
+            // copies of the final piece there
+            for (int z = lane; z < (4 * kSteps - nbI) * (kImgBytes / 16); z += 64)
+              reinterpret_cast<i32x4*>(wimg + (size_t)nbI * kImgBytes)[z] = i32x4{0, 0, 0, 0};
+            for (int z = nbI + lane; z < 4 * kSteps; z += 64) wsc[z] = 0u;
             __builtin_amdgcn_wave_barrier();
           }
           TRACE(4);
           XTRACE(wave);  // per wave: image in LDS
-          d = mfma_chain(rd, sh, S, nbI, wimg, wsc, lds_zero, i, g, d);
+          d = mfma_chain_p(rd, wimg, wsc, i, g);
           XTRACE(4 + wave);  // per wave: chain done
         }
 #pragma unroll

@@ -76,16 +76,20 @@ __device__ __forceinline__ void load_b(const uint8_t* img, const uint32_t* sc, c
   const int bs = min(4 * st + g, nb - 1);
   // Columns past kTerms multiply a zero B operand, so any finite scale serves them: every
   // lane takes a byte of the block's scale word (bytes are <= 247, never the NaN code 0xFF),
-  // with no branch around the LDS load.
-  sb = (int)((sc[bs] >> (8 * (i & 3))) & 0xFFu);
+  // with no branch around the LDS load. A byte load: the value needs no ALU step, which the
+  // scheduler would otherwise hoist above the previous MFMA together with a wait for it.
+  sb = (int)reinterpret_cast<const uint8_t*>(sc)[bs * 4 + (i & 3)];
 }
 
 // Raw 20-byte window (5 aligned dwords) holding one 17-byte block.
 struct RawBlk {
   uint32_t d[5];
 };
+// Global (not flat) loads: a flat load also counts on the LDS counter, so a later wait for
+// its data would also wait for every LDS read issued meanwhile.
 __device__ __forceinline__ void raw_load(const uint8_t* p, RawBlk& r) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
+  const __attribute__((address_space(1))) uint32_t* w =
+      (const __attribute__((address_space(1))) uint32_t*)(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
   r.d[0] = w[0], r.d[1] = w[1], r.d[2] = w[2], r.d[3] = w[3], r.d[4] = w[4];
 }
 __device__ __forceinline__ void raw_zero(RawBlk& r) { r.d[0] = r.d[1] = r.d[2] = r.d[3] = r.d[4] = 0u; }
@@ -121,16 +125,14 @@ __device__ __forceinline__ f32x4 mfma_op(const AOp& a, int sa, const i32x8& B, i
 // start at byte sh+1 of the window.
 __device__ __forceinline__ f32x4 mfma_raw(const RawBlk& r, uint32_t sh, bool valid, const i32x8& B,
                                           int sb, f32x4 acc) {
+  // selects, not a branch: a divergent branch per step splits the chain into basic blocks,
+  // across which the compiler reorders the MFMAs away from their operands
   const uint32_t t = sh + 1u;
-  uint32_t q0, q1, q2, q3;
-  if (t == 4u) {
-    q0 = r.d[1], q1 = r.d[2], q2 = r.d[3], q3 = r.d[4];
-  } else {
-    q0 = __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
-    q1 = __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
-    q2 = __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
-    q3 = __builtin_amdgcn_alignbyte(r.d[4], r.d[3], t);
-  }
+  const bool hi = t == 4u;
+  const uint32_t q0 = hi ? r.d[1] : __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
+  const uint32_t q1 = hi ? r.d[2] : __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
+  const uint32_t q2 = hi ? r.d[3] : __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
+  const uint32_t q3 = hi ? r.d[4] : __builtin_amdgcn_alignbyte(r.d[4], r.d[3], t);
   const int sa = valid ? (int)((r.d[0] >> (8u * sh)) & 0xFFu) : 127;
   const i32x8 A = {(int)q0, (int)q1, (int)q2, (int)q3, 0, 0, 0, 0};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, sa, 0, sb);
@@ -161,6 +163,6 @@ __device__ __forceinline__ void load_b_fast(const uint8_t* base, const uint32_t*
   const i32x4 v0 = *reinterpret_cast<const i32x4*>(base + b0 * kImgBytes);
   const i32x4 v1 = *reinterpret_cast<const i32x4*>(base + b1 * kImgBytes);
   B = i32x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-  sb = (int)((sc[min(4 * st + g, nb - 1)] >> (8 * (i & 3))) & 0xFFu);
+  sb = (int)reinterpret_cast<const uint8_t*>(sc)[min(4 * st + g, nb - 1) * 4 + (i & 3)];
 }
 }  // namespace mr
