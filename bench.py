@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--kernel", default="auto", choices=["auto", "valu", "fused"])
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-prefetch-hint", action="store_true",
+                    help="do not link each layer to the next (mr_layer_set_next)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=16)
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -228,6 +230,9 @@ def main():
     layers = [W.DeviceLayer(ctx, s) for s in specs]
     for dl in layers:
         dl.layer.reserve(1)
+    if not a.no_prefetch_hint:  # decode order: layer l, then l+1; the last, then the next token's first
+        for li, dl in enumerate(layers):
+            dl.layer.set_next(layers[(li + 1) % n_layers].layer)
     log(f"built {n_layers} layers in {time.perf_counter() - t0:.1f}s")
     H = specs[0].hidden
     # inputs: x[token][layer] resident in HBM before the timed region
@@ -345,7 +350,8 @@ def main():
         "config": {"workload": W.CONFIG_NAMES[a.config], "config_id": a.config,
                    "layers": n_layers, "tokens": K, "hidden": s0.hidden, "inter": s0.inter,
                    "experts": [s.n_experts for s in specs][:1] if a.config != 4 else "256..512",
-                   "top_k": s0.top_k, "graph": not a.no_graph, "kernel": a.kernel},
+                   "top_k": s0.top_k, "graph": not a.no_graph, "kernel": a.kernel,
+                   "next_layer_hint": not a.no_prefetch_hint},
         "hbm_gbs": round(K / (ms / 1e3) * bytes_per_token / 1e9, 1),
         "hbm_frac": round(K / (ms / 1e3) * bytes_per_token / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_token": bytes_per_token,

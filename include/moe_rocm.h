@@ -161,6 +161,14 @@ typedef struct mr_layer_desc {
 
 int mr_layer_create(mr_ctx* ctx, const mr_layer_desc* desc, mr_layer** out);
 void mr_layer_destroy(mr_layer* layer);
+/* Prefetch hint (no reference counterpart; the reference's decode loop runs the
+ * layers in order, layer.rs:756-1980 per layer): `next` is the layer whose
+ * mr_moe_forward follows this layer's. While this layer's fused decode kernel
+ * streams expert weights, its router workgroups read the next layer's router
+ * rows, so the next layer's router step finds them in the caches instead of
+ * HBM. Results do not change. NULL clears the hint; `next` must belong to the
+ * same context and stay alive (or be cleared here) while this layer is used. */
+int mr_layer_set_next(mr_layer* layer, const mr_layer* next);
 /* Allocate context scratch for up to max_tokens tokens of this layer's shape
  * (BatchedMoeBuffers::new, metal/mod.rs:1240). Call before graph capture. */
 int mr_reserve(mr_ctx* ctx, const mr_layer* layer, uint32_t max_tokens);

@@ -528,6 +528,13 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   return MR_OK;
 }
 
+int mr_layer_set_next(mr_layer* L, const mr_layer* next) {
+  if (!L) return set_err(nullptr, MR_E_INVAL, "mr_layer_set_next: layer is NULL");
+  if (next && next->ctx != L->ctx) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_next: layers of different contexts");
+  L->next = next;
+  return MR_OK;
+}
+
 void mr_layer_destroy(mr_layer* L) {
   if (!L) return;
   if (L->fused_sync && has_dev(L->ctx)) {

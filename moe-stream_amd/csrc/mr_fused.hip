@@ -81,6 +81,7 @@ struct FusedArgs {
   int R, NG, ND;
   uint32_t spin_limit;
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
+  PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
   unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][16] timestamps
 };
 
@@ -396,6 +397,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       put_logit(a.fs, (uint32_t)a.E, e, seq, acc);
     }
     TRACE(1);
+    prefetch_rows(a.pf, bid, a.R, lds_dyn);
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
@@ -431,6 +433,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     if (wave == 0 && !route_wave(rc, seq, sel_i, sel_w, sel_o)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
+    XTRACE(wave);  // per wave: at the routing barrier
     __syncthreads();  // routing and x image ready
     TRACE(2);
     if (ok_flag && gid < a.NG) {  // one unit per workgroup
@@ -457,6 +460,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       f32x4 dacc = stream_chain(W, rb, S, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
                                 lds_zero, lane, i, g);
 #endif
+      XTRACE(4 + wave);  // per wave: chain done
       TRACE(3);
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
@@ -511,6 +515,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       int slot = wave;
       const uint8_t* D = a.down + a.down_off[sel_i[slot < a.k ? slot : 0]] + (uint64_t)row * rb;
       if (slot < a.k) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
+      // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
+      int so[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) so[p] = sel_o[min(p, a.k - 1)] * 16;
       // this thread's output-row bias terms, also independent of gate/up
       float ybias = 0.f;
       if (tid < 16 && a.down_b)
@@ -563,7 +571,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         if (tid < 16) {
           const int rr = q * 16 + tid;
           float yv = 0.f;  // slots in ascending expert order (layer.rs:1092-1106)
-          for (int p = 0; p < a.k; ++p) yv = yv + lds_part[sel_o[p] * 16 + tid];
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            if (p < a.k) yv = yv + lds_part[so[p] + tid];
           yv = yv + ybias;
           if (rr < a.H) a.y[rr] = yv;
           XTRACE(8);
@@ -620,6 +630,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.NG = (int)(k * nbI);
   a.ND = (int)((L.H + 15) / 16);
   a.spin_limit = spin_limit;
+  a.pf = prefetch_plan(L.next);
   // gate/up: x image (nbH blocks); down: one padded slot image per wave
   const uint64_t img_bytes = std::max<uint64_t>(nbH * kImgBytes, 4ull * kImgVec * 1024);
   const uint64_t sc_words = std::max<uint64_t>(nbH, 4ull * 128);

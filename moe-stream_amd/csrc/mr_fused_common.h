@@ -16,6 +16,7 @@
 
 #include "../../include/moe_rocm.h"
 #include "mr_device.h"
+#include "mr_internal.h"
 
 namespace mr {
 
@@ -196,6 +197,44 @@ __device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t targ
     if (it >= limit) return false;
     __builtin_amdgcn_s_sleep(SLEEP);
   }
+}
+
+// ---- next-layer router prefetch -----------------------------------------------------------
+// Router rows of the layer that runs next (rows 0..E-1 of its router weights, then its
+// shared-expert gate row if it has one). Its router workgroup b reads rows 4b..4b+3; router
+// workgroup b of this launch reads the rows of next workgroups b, b + R, ... into LDS and
+// drops them, after publishing its own logits, so they are in the caches when the next
+// launch starts (workgroup b runs on XCD b mod 8 in both launches).
+struct PrefetchRows {
+  const float* w;   // [E, H] f32, or nullptr: no prefetch
+  const float* sh;  // row E (shared-expert gate) or nullptr
+  int rows, E, H;
+};
+__device__ __forceinline__ void prefetch_rows(const PrefetchRows& p, int bid, int R, uint8_t* lds) {
+  if (!p.w) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int nb = bid; nb * 4 < p.rows; nb += R) {
+    const int e = nb * 4 + wave;
+    if (e < p.rows) {
+      const float* src = e < p.E ? p.w + (size_t)e * p.H : p.sh;
+      for (int j = 0; j * 256 < p.H; ++j) {  // 64 lanes x 16 bytes per load
+        const int c = min(j * 256 + lane * 4, p.H - 4);
+        __builtin_amdgcn_global_load_lds(src + c, lds + wave * 1024, 16, 0, 0);
+      }
+    }
+  }
+  vm_drain();  // the loads complete before this workgroup's LDS is released
+}
+// Host side: the plan for the hint set with mr_layer_set_next (no prefetch without one).
+inline PrefetchRows prefetch_plan(const mr_layer* n) {
+  PrefetchRows p{nullptr, nullptr, 0, 0, 0};
+  if (!n || !n->d.router_w || n->H < 4) return p;
+  p.w = n->d.router_w;
+  p.sh = n->d.sh_gate ? n->d.sh_gate_inp : nullptr;
+  p.E = (int)n->E;
+  p.rows = (int)n->E + (p.sh ? 1 : 0);
+  p.H = (int)n->H;
+  return p;
 }
 
 // ---- routing ----------------------------------------------------------------------------

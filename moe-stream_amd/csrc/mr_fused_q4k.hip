@@ -102,6 +102,7 @@ struct Q4Args {
   float alpha, limit;
   int R, ND, NG;
   uint32_t spin_limit;
+  PrefetchRows pf;  // the next layer's router rows (router workgroups read them)
   unsigned long long* trace;
 };
 
@@ -287,6 +288,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       put_logit(a.fs, (uint32_t)(a.E + a.has_sh), e, seq, acc);
     }
     TRACE(1);
+    prefetch_rows(a.pf, bid, a.R, smem);
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
@@ -516,6 +518,7 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
   a.ND = (int)(L.H / 8);
   a.NG = (int)((uint64_t)a.ktot * nGI);
   a.spin_limit = L.ctx->spin_limit;
+  a.pf = prefetch_plan(L.next);
   ProfScope ps(K, "fused_layer");
   hipLaunchKernelGGL(k_fused_q4k, dim3(a.R + a.ND + a.NG), dim3(256), 0, K.s, a);
   return hipGetLastError();

@@ -112,6 +112,7 @@ struct mr_layer {
   uint32_t H = 0, I = 0, E = 0, Ish = 0;
   int type = 0;
   uint32_t* fused_sync = nullptr;  // device sync block of the fused decode kernel
+  const mr_layer* next = nullptr;  // layer run after this one (router prefetch hint) or NULL
 };
 
 struct mr_graph {

@@ -73,6 +73,7 @@ _SIGS = {
     "mr_dequant": (C.c_int, [_vp, _vp, _u32, _vp]),
     "mr_layer_create": (C.c_int, [_vp, C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "mr_layer_destroy": (None, [_vp]),
+    "mr_layer_set_next": (C.c_int, [_vp, _vp]),
     "mr_reserve": (C.c_int, [_vp, _vp, _u32]),
     "mr_router_topk": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "mr_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp]),
@@ -306,6 +307,12 @@ class MoeLayer:
         self.n_experts, self.top_k = gate.n_experts, top_k
         self._refs = (gate, up, down, router_w, router_b, dummy_mask, gate_bias, up_bias,
                       down_bias, sh_gate, sh_up, sh_down, sh_gate_inp)
+        self._next = None
+
+    def set_next(self, nxt: "MoeLayer | None") -> None:
+        """Prefetch hint: `nxt` runs after this layer (mr_layer_set_next); results do not change."""
+        self.ctx.check(_lib.mr_layer_set_next(self.h, nxt.h if nxt is not None else None))
+        self._next = nxt  # keeps the next layer alive while this one may prefetch it
 
     def reserve(self, max_tokens: int) -> None:
         self.ctx.check(_lib.mr_reserve(self.ctx.h, self.h, max_tokens))
@@ -328,6 +335,7 @@ class MoeLayer:
         if self.h:
             _lib.mr_layer_destroy(self.h)
             self.h = None
+            self._next = None
 
 
 def topk(ctx: Context, logits, n_tokens: int, n_experts: int, top_k: int, flags: int, idx, w) -> None:

@@ -153,3 +153,23 @@ def test_matrix_bytes():
     assert M.matrix_bytes(M.GGML_Q4_K, 768, 2048) == 884_736
     assert M.matrix_bytes(M.GGML_Q4_K, 2048, 512) == 589_824
     assert M.matrix_bytes(99, 1, 1) == 0
+
+
+def test_set_next_validation(hctx):
+    g, u, d = _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 128, 64)
+    L1 = M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x1000, route_flags=1, act=1)
+    L2 = M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x2000, route_flags=1, act=1)
+    L1.set_next(L2)  # a hint: no device work, valid on a host-only context
+    L1.set_next(L1)  # a layer may follow itself (one-layer loops)
+    L1.set_next(None)
+    assert M.lib.mr_layer_set_next(None, None) == M.MR_E_INVAL
+    other = M.Context(M.DEVICE_NONE)
+    try:
+        g2, u2, d2 = _mx_pack(other, 4, 64, 128), _mx_pack(other, 4, 64, 128), _mx_pack(other, 4, 128, 64)
+        L3 = M.MoeLayer(other, g2, u2, d2, top_k=2, router_w=0x3000, route_flags=1, act=1)
+        with pytest.raises(M.MoeRocmError) as ei:
+            L1.set_next(L3)
+        assert ei.value.status == M.MR_E_INVAL and "different contexts" in ei.value.message
+        L3.close()
+    finally:
+        other.close()

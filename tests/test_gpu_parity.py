@@ -380,3 +380,34 @@ def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers, name):
     assert np.array_equal(dy.download(np.float32), ref)
     print(f"forced-timeout launches reporting an error: {errors} of 5")
     dx.free(), dy.free()
+
+
+# (layer, next layer) pairs: same type, MXFP4 -> Q4_K with a shared-expert gate row, Q4_K -> MXFP4
+NEXT_PAIRS = [("C1-gpt-oss", "C1-gpt-oss"), ("tiny-mxfp4", "tiny-q4k-shared"),
+              ("tiny-q4k-shared", "tiny-mxfp4"), ("C3-qwen3-layer0", "C4-coder-next-layer0")]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pair", NEXT_PAIRS, ids=lambda p: f"{p[0]}->{p[1]}")
+def test_next_layer_hint_keeps_results(gpu_ctx, layers, pair):
+    """mr_layer_set_next only prefetches the next layer's router rows: both layers'
+    outputs are bitwise the same with and without the hint, and clearing it works."""
+    a, b = (get_layer(gpu_ctx, layers, n)[0] for n in pair)
+    xa = gpu_ctx.to_device(W.x_tokens(a.spec, 1, first_token=90)[0])
+    xb = gpu_ctx.to_device(W.x_tokens(b.spec, 1, first_token=91)[0])
+    ya, yb = gpu_ctx.alloc(a.spec.hidden * 4), gpu_ctx.alloc(b.spec.hidden * 4)
+    a.layer.forward(xa, ya), b.layer.forward(xb, yb)
+    ref_a, ref_b = ya.download(np.float32), yb.download(np.float32)
+    try:
+        a.layer.set_next(b.layer)
+        for _ in range(3):
+            a.layer.forward(xa, ya), b.layer.forward(xb, yb)
+            gpu_ctx.sync()
+            assert np.array_equal(ya.download(np.float32), ref_a)
+            assert np.array_equal(yb.download(np.float32), ref_b)
+    finally:
+        a.layer.set_next(None)
+    a.layer.forward(xa, ya)
+    assert np.array_equal(ya.download(np.float32), ref_a)
+    for t in (xa, xb, ya, yb):
+        t.free()
