@@ -192,6 +192,13 @@ int mr_moe_experts(mr_ctx* ctx, const mr_layer* layer, const float* x, uint32_t 
  * expert; no host synchronisation. Replaces gpu_routed_moe_forward_metal
  * (metal/mod.rs:1512-1677) and the CPU run_moe path (layer.rs:756-1980). */
 int mr_moe_forward(mr_ctx* ctx, const mr_layer* layer, const float* x, float* y);
+/* mr_moe_forward with the steps on either side of it fused in (layer.rs:462-473):
+ * the input is rms_norm(h) = (h * inv) * norm_w, inv = 1 / sqrt(mean(h^2) + eps)
+ * (ops/norm.rs:16-37, the post-attention norm), and h_out = h + moe(rms_norm(h))
+ * (the residual add). h_out may equal h (in place). h, norm_w, h_out: [H] f32,
+ * 16-byte aligned; 0 <= eps <= 1. */
+int mr_moe_forward_residual(mr_ctx* ctx, const mr_layer* layer, const float* h, const float* norm_w,
+                            float eps, float* h_out);
 /* Whole layer for n_tokens tokens (prefill / batched): tokens are grouped by
  * expert and each expert's weights are read once for all its tokens.
  * Replaces the multi-token paths layer.rs:1449-1514 and 2148-2183. */

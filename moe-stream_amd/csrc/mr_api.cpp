@@ -100,7 +100,7 @@ int upload_offsets(mr_ctx* c, mr_pack* p) {
 
 // Scratch layout for T tokens of a layer shape.
 struct ScratchPlan {
-  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, grouped, total;
+  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, grouped, xn, ytmp, total;
 };
 
 ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
@@ -117,6 +117,8 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
   p.grouped = o, o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
+  p.xn = o, o += align_up(T * H * 4);
+  p.ytmp = o, o += align_up(T * H * 4);
   p.total = o;
   return p;
 }
@@ -160,6 +162,8 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   s.sync = reinterpret_cast<uint32_t*>(b + p.sync);
   s.groups = reinterpret_cast<int32_t*>(b + p.groups);
   s.grouped = b + p.grouped;
+  s.xn = reinterpret_cast<float*>(b + p.xn);
+  s.ytmp = reinterpret_cast<float*>(b + p.ytmp);
   s.cap_tokens = nT, s.cap_k = nk, s.cap_e = nE, s.cap_i = nI, s.cap_h = nH, s.cap_ish = nS;
   return MR_OK;
 }
@@ -599,15 +603,11 @@ int mr_moe_experts(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, con
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "expert launch");
 }
 
-int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
-  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
-  int rc = check_layer(c, L);
-  if (rc) return rc;
-  if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
-  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+// One decode token through the layer. nr.w != nullptr: the input is rms_norm(x) and the
+// output is x + moe(rms_norm(x)) (mr_moe_forward_residual); y may then alias x.
+static int forward_one(mr_ctx* c, const mr_layer* L, const float* x, float* y, const mr::NormResid& nr) {
+  int rc;
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, 1))) return rc;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u)
-    return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
   mr::Scratch& s = c->scratch;
   hipError_t e;
   if (c->decode_kernel != MR_DECODE_VALU && L->fused_sync) {
@@ -615,21 +615,55 @@ int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
     uint8_t* img = static_cast<uint8_t*>(s.mfma_b);
     if (mr::fused_supported(*L, c->n_cu)) {
       c->fused_used = true;
-      e = mr::launch_fused(c->launch(), *L, x, y, err, img, c->spin_limit, c->n_cu);
+      e = mr::launch_fused(c->launch(), *L, x, y, err, img, c->spin_limit, c->n_cu, nr);
       return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
     }
     if (mr::fused_q4k_supported(*L, c->n_cu)) {
       c->fused_used = true;
-      e = mr::launch_fused_q4k(c->launch(), *L, x, y, err, img);
+      e = mr::launch_fused_q4k(c->launch(), *L, x, y, err, img, nr);
       return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
     }
   }
   if (c->decode_kernel == MR_DECODE_FUSED)
     return set_err(c, MR_E_UNSUPPORTED, "the fused decode kernels do not cover this layer shape");
-  e = mr::launch_router_logits(c->launch(), *L, x, 1, s.logits);
+  const float* xin = x;
+  float* yout = y;
+  e = hipSuccess;
+  if (nr.w) {
+    e = mr::launch_rms_norm(c->launch(), x, nr.w, nr.eps, 1, L->H, s.xn);
+    xin = s.xn, yout = s.ytmp;
+  }
+  if (e == hipSuccess) e = mr::launch_router_logits(c->launch(), *L, xin, 1, s.logits);
   if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
-  if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, x, 1, s.idx, s.w, s.act, s.act_sh, y);
+  if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, xin, 1, s.idx, s.w, s.act, s.act_sh, yout);
+  if (e == hipSuccess && nr.w) e = mr::launch_residual_add(c->launch(), x, s.ytmp, L->H, y);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "moe forward launch");
+}
+
+int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u)
+    return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
+  return forward_one(c, L, x, y, mr::NormResid{});
+}
+
+int mr_moe_forward_residual(mr_ctx* c, const mr_layer* L, const float* h, const float* norm_w, float eps,
+                            float* h_out) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!h || !norm_w || !h_out) return set_err(c, MR_E_INVAL, "NULL h, norm_w or h_out");
+  if (!(eps >= 0.f) || eps > 1.f) return set_err(c, MR_E_INVAL, "eps %g is not in [0, 1]", (double)eps);
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(h_out)) & 15u)
+    return set_err(c, MR_E_INVAL, "h, norm_w and h_out must be 16-byte aligned");
+  mr::NormResid nr;
+  nr.w = norm_w, nr.eps = eps, nr.resid = h;
+  return forward_one(c, L, h, h_out, nr);
 }
 
 int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {

@@ -82,6 +82,7 @@ struct FusedArgs {
   uint32_t spin_limit;
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
+  NormResid nr;               // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
   unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][16] timestamps
 };
 
@@ -346,6 +347,9 @@ __device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, i
 }
 
 // ---- the kernel ----------------------------------------------------------------------------
+// NORM: the input is rms_norm(x) and the residual x is added to y (mr_moe_forward_residual);
+// a separate instantiation, so the plain decode path compiles without that code.
+template <bool NORM>
 __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   extern __shared__ __align__(16) uint8_t lds_dyn[];
   uint8_t* lds_img = lds_dyn;
@@ -383,6 +387,15 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
         wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
       }
+      if (NORM) {  // x = rms_norm(h)
+        f32x4 nv[kRouterVec];
+        load_lanes4(a.nr.w, a.H, nv);
+        const float inv = rms_inv(xv, a.H, a.nr.eps);
+#pragma unroll
+        for (int j = 0; j < kRouterVec; ++j)
+          xv[j] = f32x4{norm1(xv[j].x, inv, nv[j].x), norm1(xv[j].y, inv, nv[j].y),
+                        norm1(xv[j].z, inv, nv[j].z), norm1(xv[j].w, inv, nv[j].w)};
+      }
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < kRouterVec; ++j) {
@@ -414,6 +427,24 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         const float* xb = a.x + b * 32 + 2 * m;
         lo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb) : f32x2{0.f, 0.f};        // 2m, 2m+1
         hi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb + 16) : f32x2{0.f, 0.f};   // 2m+16, 2m+17
+      }
+      if (NORM) {  // x = rms_norm(h): each wave derives inv the way the router waves do
+        f32x4 hv[kRouterVec];
+        load_lanes4(a.x, a.H, hv);
+        f32x2 nlo[kRounds], nhi[kRounds];
+#pragma unroll
+        for (int j = 0; j < kRounds; ++j) {
+          const int b = (tid >> 3) + 32 * j;
+          const float* wb = a.nr.w + b * 32 + 2 * m;
+          nlo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(wb) : f32x2{0.f, 0.f};
+          nhi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(wb + 16) : f32x2{0.f, 0.f};
+        }
+        const float inv = rms_inv(hv, a.H, a.nr.eps);
+#pragma unroll
+        for (int j = 0; j < kRounds; ++j) {
+          lo[j] = f32x2{norm1(lo[j].x, inv, nlo[j].x), norm1(lo[j].y, inv, nlo[j].y)};
+          hi[j] = f32x2{norm1(hi[j].x, inv, nhi[j].x), norm1(hi[j].y, inv, nhi[j].y)};
+        }
       }
 #pragma unroll
       for (int j = 0; j < kRounds; ++j) {
@@ -519,7 +550,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       int so[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) so[p] = sel_o[min(p, a.k - 1)] * 16;
-      // this thread's output-row bias terms, also independent of gate/up
+      // this thread's output-row bias terms and residual, also independent of gate/up
+      const float yres = (tid < 16 && NORM && q * 16 + tid < a.H) ? a.nr.resid[q * 16 + tid] : 0.f;
       float ybias = 0.f;
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
@@ -575,6 +607,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           for (int p = 0; p < 4; ++p)
             if (p < a.k) yv = yv + lds_part[so[p] + tid];
           yv = yv + ybias;
+          if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
           if (rr < a.H) a.y[rr] = yv;
           XTRACE(8);
         }
@@ -611,7 +644,8 @@ extern "C" void mr_debug_fused_trace(void* dev_buf) { g_fused_trace = (unsigned 
 #endif
 
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu) {
+                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
+                        const NormResid& nr) {
   FusedArgs a{};
 #ifdef MR_FUSED_TRACE
   a.trace = g_fused_trace;
@@ -631,13 +665,17 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.ND = (int)((L.H + 15) / 16);
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
+  a.nr = nr;
   // gate/up: x image (nbH blocks); down: one padded slot image per wave
   const uint64_t img_bytes = std::max<uint64_t>(nbH * kImgBytes, 4ull * kImgVec * 1024);
   const uint64_t sc_words = std::max<uint64_t>(nbH, 4ull * 128);
   a.lds_img_bytes = (uint32_t)img_bytes;
   const size_t lds = img_bytes + sc_words * 4;
   ProfScope ps(K, "fused_layer");
-  hipLaunchKernelGGL(k_fused_mxfp4, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
+  if (nr.w)
+    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
+  else
+    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
   return hipGetLastError();
 }
 

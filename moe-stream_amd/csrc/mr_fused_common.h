@@ -199,6 +199,42 @@ __device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t targ
   }
 }
 
+// ---- fused RMSNorm and residual (norm.rs:16-37; layer.rs:462-473) ---------------------------
+// mr_moe_forward_residual: the layer's input is rms_norm(h) = (h * inv) * w with
+// inv = 1 / sqrt(mean(h^2) + eps), and its output is h + moe(rms_norm(h)). w == nullptr: the
+// input is used as given and nothing is added.
+// (NormResid, the launch argument, is declared with the launchers.)
+// inv of the RMSNorm from a wave's lane-strided float4s of h (lane l holds elements
+// 4*(l + 64*j) .. +3, zero past H): squares rounded, then summed in a fixed order per lane
+// and a butterfly across lanes, so every wave that calls this gets the same bits.
+// (No contraction: squares and sums are rounded separately; sqrtf and the division are
+// the correctly rounded HIP forms.)
+template <int NV>
+__device__ __forceinline__ float rms_inv(const f32x4 (&xv)[NV], int H, float eps) {
+#pragma clang fp contract(off)
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    s = s + xv[j].x * xv[j].x;
+    s = s + xv[j].y * xv[j].y;
+    s = s + xv[j].z * xv[j].z;
+    s = s + xv[j].w * xv[j].w;
+  }
+  s = wave_sum(s);  // the same bits in every lane
+  return 1.f / sqrtf(s / (float)H + eps);
+}
+// A wave's lane-strided float4s of v (zero past H).
+template <int NV>
+__device__ __forceinline__ void load_lanes4(const float* v, int H, f32x4 (&out)[NV]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    out[j] = c < H ? *reinterpret_cast<const f32x4*>(v + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+__device__ __forceinline__ float norm1(float x, float inv, float w) { return (x * inv) * w; }
+
 // ---- next-layer router prefetch -----------------------------------------------------------
 // Router rows of the layer that runs next (rows 0..E-1 of its router weights, then its
 // shared-expert gate row if it has one). Its router workgroup b reads rows 4b..4b+3; router

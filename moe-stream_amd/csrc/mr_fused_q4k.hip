@@ -103,6 +103,7 @@ struct Q4Args {
   int R, ND, NG;
   uint32_t spin_limit;
   PrefetchRows pf;  // the next layer's router rows (router workgroups read them)
+  NormResid nr;     // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
   unsigned long long* trace;
 };
 
@@ -239,6 +240,9 @@ __device__ __forceinline__ void region_load(const uint8_t* base, int nsb, uint4 
   }
 }
 
+// NORM: the input is rms_norm(x) and the residual x is added to y (mr_moe_forward_residual);
+// a separate instantiation, so the plain decode path compiles without that code.
+template <bool NORM>
 __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   __shared__ __align__(16) uint8_t smem[kQ4Smem];
   __shared__ int sel_i[16];
@@ -272,6 +276,15 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
         wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
       }
+      if (NORM && w) {  // x = rms_norm(h)
+        f32x4 nv[kQ4RouterVec];
+        load_lanes4(a.nr.w, a.H, nv);
+        const float inv = rms_inv(xv, a.H, a.nr.eps);
+#pragma unroll
+        for (int j = 0; j < kQ4RouterVec; ++j)
+          xv[j] = f32x4{norm1(xv[j].x, inv, nv[j].x), norm1(xv[j].y, inv, nv[j].y),
+                        norm1(xv[j].z, inv, nv[j].z), norm1(xv[j].w, inv, nv[j].w)};
+      }
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < kQ4RouterVec; ++j) {
@@ -294,6 +307,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     const int gid = bid - a.R - a.ND;
     uint8_t* xq = smem + kGuXq;
     float2* xs = reinterpret_cast<float2*>(smem + kGuXs);
+    // x = rms_norm(h) when fused: each wave derives inv the way the router waves do
+    float inv = 1.f;
+    if (NORM) {
+      f32x4 hv[kQ4RouterVec];
+      load_lanes4(a.x, a.H, hv);
+      inv = rms_inv(hv, a.H, a.nr.eps);
+    }
     // x image: one 16-element group per thread
     for (int G = tid; G < (a.H >> 4); G += 256) {
       float v[16];
@@ -301,6 +321,14 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       for (int q = 0; q < 4; ++q) {
         const f32x4 t = *reinterpret_cast<const f32x4*>(a.x + G * 16 + 4 * q);
         v[4 * q] = t.x, v[4 * q + 1] = t.y, v[4 * q + 2] = t.z, v[4 * q + 3] = t.w;
+      }
+      if (NORM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 nw = *reinterpret_cast<const f32x4*>(a.nr.w + G * 16 + 4 * q);
+          v[4 * q] = norm1(v[4 * q], inv, nw.x), v[4 * q + 1] = norm1(v[4 * q + 1], inv, nw.y);
+          v[4 * q + 2] = norm1(v[4 * q + 2], inv, nw.z), v[4 * q + 3] = norm1(v[4 * q + 3], inv, nw.w);
+        }
       }
       float m = 0.f, sum = 0.f;
 #pragma unroll
@@ -405,6 +433,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         const uint8_t* D = sc >= a.k ? a.sh_down : a.down + a.down_off[sel_i[sc]];
         if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, nsbI, ch[j]);
       }
+      const float yres = (tid < 8 && NORM && q * 8 + tid < a.H) ? a.nr.resid[q * 8 + tid] : 0.f;
       float ybias = 0.f;  // this row's routed bias terms (layer.rs:1417-1444)
       if (tid < 8 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 8 + tid];
@@ -459,6 +488,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
           for (int p = 0; p < a.k; ++p) yv = yv + dn_part[sel_o[p]][tid];
           yv = yv + ybias;
           if (a.has_sh) yv = yv + dn_part[a.k][tid];  // shared expert after the routed sum
+          if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
           if (rr < a.H) a.y[rr] = yv;
         }
       }
@@ -492,7 +522,7 @@ bool fused_q4k_supported(const mr_layer& L, int n_cu) {
 }
 
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
-                            uint8_t* img_base) {
+                            uint8_t* img_base, const NormResid& nr) {
   Q4Args a{};
 #ifdef MR_FUSED_TRACE
   a.trace = g_fused_trace;
@@ -519,8 +549,12 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
   a.NG = (int)((uint64_t)a.ktot * nGI);
   a.spin_limit = L.ctx->spin_limit;
   a.pf = prefetch_plan(L.next);
+  a.nr = nr;
   ProfScope ps(K, "fused_layer");
-  hipLaunchKernelGGL(k_fused_q4k, dim3(a.R + a.ND + a.NG), dim3(256), 0, K.s, a);
+  if (nr.w)
+    hipLaunchKernelGGL(k_fused_q4k<true>, dim3(a.R + a.ND + a.NG), dim3(256), 0, K.s, a);
+  else
+    hipLaunchKernelGGL(k_fused_q4k<false>, dim3(a.R + a.ND + a.NG), dim3(256), 0, K.s, a);
   return hipGetLastError();
 }
 

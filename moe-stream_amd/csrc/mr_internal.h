@@ -31,6 +31,8 @@ struct Scratch {
   uint32_t* sync = nullptr;    // sync words for the fused decode kernel
   int32_t* groups = nullptr;   // batched path: per-expert token lists
   void* grouped = nullptr;     // grouped MFMA path: activation images and per-pair outputs
+  float* xn = nullptr;         // [T, H] normalised input (mr_moe_forward_residual, multi-kernel path)
+  float* ytmp = nullptr;       // [T, H] MoE output before the residual add
   uint64_t cap_tokens = 0, cap_k = 0, cap_e = 0, cap_i = 0, cap_h = 0, cap_ish = 0;
 };
 
@@ -132,13 +134,25 @@ hipError_t launch_experts_valu(const Launch& K, const mr_layer& L, const float* 
                                const int32_t* idx, const float* w, float* act, float* act_sh,
                                float* y);
 hipError_t launch_dequant(const Launch& K, const mr_pack& p, uint32_t expert, float* out);
+hipError_t launch_rms_norm(const Launch& K, const float* h, const float* w, float eps, uint32_t T, uint32_t H,
+                           float* out);
+hipError_t launch_residual_add(const Launch& K, const float* h, const float* m, uint64_t n, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+
+// Fused RMSNorm of the layer input and residual added to its output
+// (mr_moe_forward_residual; norm.rs:16-37, layer.rs:462-473). w == nullptr: off.
+struct NormResid {
+  const float* w = nullptr;      // [H] norm weight
+  float eps = 0.f;
+  const float* resid = nullptr;  // [H] residual h (the un-normalised input)
+};
 
 // Fused single-launch MXFP4 decode layer (mr_fused.hip).
 constexpr int kSyncErrWord = 96;  // uint32 index of the fused kernel's error word
 bool fused_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu);
+                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
+                        const NormResid& nr = NormResid{});
 uint64_t fused_layer_sync_bytes();
 
 // Scratch of the grouped multi-token MXFP4 path (device pointers; P = T * top_k pairs).
@@ -162,7 +176,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
                           const float* w, float* y, const GroupedScratch& gs);
 bool fused_q4k_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
-                            uint8_t* img_base);
+                            uint8_t* img_base, const NormResid& nr = NormResid{});
 #ifdef MR_FUSED_TRACE
 extern unsigned long long* g_fused_trace;
 #endif

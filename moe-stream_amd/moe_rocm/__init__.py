@@ -79,6 +79,7 @@ _SIGS = {
     "mr_topk": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp]),
     "mr_moe_experts": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "mr_moe_forward": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_graph_begin": (C.c_int, [_vp]),
     "mr_graph_end": (C.c_int, [_vp, C.POINTER(_vp)]),
@@ -327,6 +328,11 @@ class MoeLayer:
 
     def forward(self, x, y) -> None:
         self.ctx.check(_lib.mr_moe_forward(self.ctx.h, self.h, _ptr(x), _ptr(y)))
+
+    def forward_residual(self, h, norm_w, eps: float, h_out) -> None:
+        """h_out = h + moe(rms_norm(h, norm_w, eps)) (mr_moe_forward_residual); h_out may be h."""
+        self.ctx.check(_lib.mr_moe_forward_residual(self.ctx.h, self.h, _ptr(h), _ptr(norm_w), eps,
+                                                    _ptr(h_out)))
 
     def forward_batched(self, x, n_tokens: int, y) -> None:
         self.ctx.check(_lib.mr_moe_forward_batched(self.ctx.h, self.h, _ptr(x), n_tokens, _ptr(y)))

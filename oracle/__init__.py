@@ -58,6 +58,7 @@ _SIGS = {
     "or_swiglu_oai1": (_f32, [_f32, _f32, _f32, _f32]),
     "or_silu_mul1": (_f32, [_f32, _f32]),
     "or_sigmoid1": (_f32, [_f32]),
+    "or_rms_norm": (None, [_vp, _vp, _sz, _sz, _f32, _vp]),
     "or_matrix_bytes": (C.c_uint64, [C.c_int, C.c_uint64, C.c_uint64]),
     "or_moe_forward": (C.c_int, [C.POINTER(OrLayer), _vp, _sz, _vp, _vp, _vp, _vp, C.c_int]),
     "or_moe_experts": (C.c_int, [C.POINTER(OrLayer), _vp, _sz, _vp, _vp, _vp, C.c_int]),
@@ -142,6 +143,16 @@ def sigmoid(x: float) -> float:
     return float(_lib.or_sigmoid1(x))
 
 
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """ops/norm.rs:32-36 over the last axis (or_rms_norm)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    width = x.shape[-1]
+    out = np.empty_like(x)
+    _lib.or_rms_norm(x.ctypes.data, w.ctypes.data, x.size // width, width, eps, out.ctypes.data)
+    return out
+
+
 class Layer:
     """Host-side copy of one MoE layer for the oracle (numpy arrays)."""
 
@@ -185,6 +196,13 @@ class Layer:
         if rc != 0:
             raise MemoryError("oracle allocation failed")
         return y, idx, w, lg
+
+    def forward_residual(self, h: np.ndarray, norm_w: np.ndarray, eps: float, n_threads: int = 1):
+        """The MoE block of a decoder layer (layer.rs:462-473): residual + moe(rms_norm(h)).
+        Returns (h_out, idx, w, logits)."""
+        h = np.ascontiguousarray(h, dtype=np.float32).reshape(-1, self.hidden)
+        y, idx, w, lg = self.forward(rms_norm(h, norm_w, eps), n_threads)
+        return h + y, idx, w, lg
 
     def experts(self, x: np.ndarray, idx: np.ndarray, w: np.ndarray, n_threads: int = 1) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.hidden)

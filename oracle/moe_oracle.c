@@ -290,6 +290,22 @@ float or_silu_mul1(float g, float u) {
 /* activation.rs:41-45: recip(exp(-x) + 1). */
 float or_sigmoid1(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
 
+/* ops/norm.rs:32-36 (CPU path): variance = mean(x^2) (sqr, then sum / n); inv_rms =
+ * recip(sqrt(variance + eps)); out = (x * inv_rms) * weight. */
+void or_rms_norm(const float* x, const float* weight, size_t n_rows, size_t width, float eps, float* out) {
+  for (size_t r = 0; r < n_rows; ++r) {
+    const float* xr = x + r * width;
+    float s = 0.0f;
+    for (size_t i = 0; i < width; ++i) {
+      const float sq = xr[i] * xr[i];
+      s = s + sq;
+    }
+    const float var = s / (float)width;
+    const float inv = 1.0f / sqrtf(var + eps);
+    for (size_t i = 0; i < width; ++i) out[r * width + i] = (xr[i] * inv) * weight[i];
+  }
+}
+
 /* ---- layer: model/layer.rs run_moe ----------------------------------------- */
 
 uint64_t or_matrix_bytes(int ggml_type, uint64_t rows, uint64_t cols) {

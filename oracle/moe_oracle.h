@@ -25,6 +25,9 @@
  *                         train.rs:1151-1184
  *   or_moe_forward        linearity in routing weights, single-expert identity,
  *                         zero-code -> bias-only, f64 numpy recomputation at tiny shapes
+ *   or_rms_norm           KAT of norm.rs:44-56 (x = 1..4, w = 1); f64 recomputation; mean of squares
+ *                         summed sequentially (candle's sum order is not reproducible here:
+ *                         order parity unpinned, value pinned to f64 within tolerance)
  *   or_f32_matvec         restates candle's F32 gemm as a sequential fp32 sum; candle's
  *                         reduction order (gemm 0.17/0.18) is not reproducible here, so the
  *                         ORDER is parity unpinned (value pinned only to f64 within tolerance)
@@ -58,6 +61,8 @@ void or_topk_routing(const float* logits, size_t n_tokens, size_t n_experts, siz
 float or_swiglu_oai1(float g, float u, float alpha, float limit);
 float or_silu_mul1(float g, float u);
 float or_sigmoid1(float x);
+/* RMSNorm of n_rows rows of width: x / sqrt(mean(x^2) + eps) * weight (ops/norm.rs:32-36). */
+void or_rms_norm(const float* x, const float* weight, size_t n_rows, size_t width, float eps, float* out);
 
 /* Bytes of one [rows, cols] matrix in a GGML block type (reader.rs:99-127). */
 uint64_t or_matrix_bytes(int ggml_type, uint64_t rows, uint64_t cols);

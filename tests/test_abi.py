@@ -173,3 +173,16 @@ def test_set_next_validation(hctx):
         L3.close()
     finally:
         other.close()
+
+
+def test_forward_residual_validation(hctx):
+    g, u, d = _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 128, 64)
+    L = M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x1000, route_flags=1, act=1)
+    for args in ((None, 0x2000, 1e-5, 0x3000), (0x1000, None, 1e-5, 0x3000), (0x1000, 0x2000, 1e-5, None),
+                 (0x1000, 0x2000, -1.0, 0x3000), (0x1000, 0x2000, float("nan"), 0x3000)):
+        with pytest.raises(M.MoeRocmError) as ei:
+            L.forward_residual(*args)
+        assert ei.value.status == M.MR_E_INVAL
+    with pytest.raises(M.MoeRocmError) as ei:
+        L.forward_residual(0x1000, 0x2000, 1e-6, 0x1000)  # valid (in place): needs a device
+    assert ei.value.status == M.MR_E_NODEV

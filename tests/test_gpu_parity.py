@@ -411,3 +411,46 @@ def test_next_layer_hint_keeps_results(gpu_ctx, layers, pair):
     assert np.array_equal(ya.download(np.float32), ref_a)
     for t in (xa, xb, ya, yb):
         t.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", FUSED)
+def test_forward_residual_matches_oracle(gpu_ctx, layers, name):
+    """mr_moe_forward_residual = h + moe(rms_norm(h)) (layer.rs:462-473, norm.rs:32-36):
+    the fused kernels and the multi-kernel path against the oracle, against each other,
+    and in place (h_out == h) bitwise equal to out of place."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec, H = dl.spec, dl.spec.hidden
+    L = oracle.layer_from_host(host)
+    rng = np.random.default_rng(1234 + H + spec.n_experts)
+    h = (W.x_tokens(spec, 2, first_token=120) * np.float32(2.5)).astype(np.float32)  # un-normalised
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    eps = 1e-5
+    dn, dh, dout = gpu_ctx.to_device(nw), gpu_ctx.alloc(H * 4), gpu_ctx.alloc(H * 4)
+    try:
+        for t in range(2):
+            dh.upload(h[t])
+            outs = {}
+            for kname, kern in (("fused", M.DECODE_FUSED), ("valu", M.DECODE_VALU)):
+                gpu_ctx.set_option(M.OPT_DECODE_KERNEL, kern)
+                dl.layer.forward_residual(dh, dn, eps, dout)
+                gpu_ctx.sync()
+                outs[kname] = dout.download(np.float32)
+            ref, _, _, rlg = L.forward_residual(h[t], nw, eps)
+            moe_ref = ref[0].astype(np.float64) - h[t]
+            scale = np.abs(moe_ref).max()
+            s = np.sort(rlg[0])[::-1]
+            if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg).max():
+                for kname, out in outs.items():
+                    err = np.abs(out.astype(np.float64) - ref[0]).max() / scale
+                    assert err <= REL_TOL, (name, t, kname, err)
+                assert np.abs(outs["fused"].astype(np.float64) - outs["valu"]).max() / scale <= 2 * REL_TOL
+            # in place, fused path: the same bits as out of place
+            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_FUSED)
+            dl.layer.forward_residual(dh, dn, eps, dh)
+            gpu_ctx.sync()
+            assert np.array_equal(dh.download(np.float32), outs["fused"])
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+    for b in (dn, dh, dout):
+        b.free()

@@ -268,3 +268,41 @@ def test_layer_zero_codes_give_bias_only():
     y = L.experts(x, idx, w)
     db = host["down_b"].reshape(8, 256)
     assert np.allclose(y[0], 0.75 * db[2] + 0.25 * db[5], rtol=1e-6, atol=1e-7)
+
+
+# ---- RMSNorm (ops/norm.rs:32-36) and the residual block (layer.rs:462-473) --------------
+def test_rms_norm_reference_kat():
+    # norm.rs:44-56: x = [1, 2, 3, 4], w = 1, eps = 1e-6 -> [0.3651, 0.7303, 1.0954, 1.4606] (+-0.01)
+    out = oracle.rms_norm(np.array([[1, 2, 3, 4]], np.float32), np.ones(4, np.float32), 1e-6)[0]
+    for got, want in zip(out, [0.3651, 0.7303, 1.0954, 1.4606]):
+        assert abs(got - want) < 0.01
+    # and the closed form: x / sqrt(7.5 + eps)
+    assert np.allclose(out, np.arange(1, 5) / math.sqrt(7.5 + 1e-6), rtol=2e-7, atol=0)
+
+
+@pytest.mark.parametrize("width", [4, 64, 2048, 2880])
+def test_rms_norm_matches_f64(width):
+    rng = np.random.default_rng(width)
+    x = rng.standard_normal((3, width)).astype(np.float32) * np.float32(3.0)
+    w = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    out = oracle.rms_norm(x, w, 1e-5)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5) * w.astype(np.float64)
+    # one sequential fp32 sum over `width` squares: relative error well below 1e-5
+    assert np.max(np.abs(out - ref) / np.abs(ref).max()) < 1e-5
+
+
+def test_rms_norm_invariants():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    a = oracle.rms_norm(x, w, 0.0)
+    # the weight multiplies last: doubling it doubles the output exactly
+    assert np.array_equal(oracle.rms_norm(x, 2 * w, 0.0), 2 * a)
+    # scale invariance (eps = 0; powers of two scale every square exactly)
+    assert np.array_equal(oracle.rms_norm(4 * x, w, 0.0), a)
+    # unit weight: the output's mean square is 1
+    u = oracle.rms_norm(x, np.ones(256, np.float32), 0.0)
+    assert np.allclose((u.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-6)
+    # eps enters under the root: a large eps shrinks the output
+    assert np.all(np.abs(oracle.rms_norm(x, w, 100.0)) < np.abs(a) + 1e-7)
