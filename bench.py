@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--kernel", default="auto", choices=["auto", "valu", "fused"])
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--residual", action="store_true",
+                    help="time mr_moe_forward_residual (post-attention RMSNorm + MoE + residual add)")
     ap.add_argument("--no-prefetch-hint", action="store_true",
                     help="do not link each layer to the next (mr_layer_set_next)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -244,9 +246,17 @@ def main():
     ctx.sync()
     xb, yb = d_x.ptr, d_y.ptr
 
+    if a.residual:  # synthetic post-attention norm weights, one vector per layer
+        rng = np.random.default_rng(20261201)
+        d_nw = ctx.to_device((1.0 + 0.1 * rng.standard_normal((n_layers, H))).astype(np.float32))
+
     def enqueue_token(t):
         for li, dl in enumerate(layers):
-            dl.layer.forward(xb + ((t * n_layers + li) * H) * 4, yb + li * H * 4)
+            if a.residual:
+                dl.layer.forward_residual(xb + ((t * n_layers + li) * H) * 4, d_nw.ptr + li * H * 4, 1e-5,
+                                          yb + li * H * 4)
+            else:
+                dl.layer.forward(xb + ((t * n_layers + li) * H) * 4, yb + li * H * 4)
 
     graphs = []
     if not a.no_graph:
@@ -351,7 +361,7 @@ def main():
                    "layers": n_layers, "tokens": K, "hidden": s0.hidden, "inter": s0.inter,
                    "experts": [s.n_experts for s in specs][:1] if a.config != 4 else "256..512",
                    "top_k": s0.top_k, "graph": not a.no_graph, "kernel": a.kernel,
-                   "next_layer_hint": not a.no_prefetch_hint},
+                   "next_layer_hint": not a.no_prefetch_hint, "fused_norm_residual": a.residual},
         "hbm_gbs": round(K / (ms / 1e3) * bytes_per_token / 1e9, 1),
         "hbm_frac": round(K / (ms / 1e3) * bytes_per_token / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_token": bytes_per_token,

@@ -80,6 +80,7 @@ typedef struct mr_ctx mr_ctx;
 typedef struct mr_pack mr_pack;
 typedef struct mr_layer mr_layer;
 typedef struct mr_graph mr_graph;
+typedef struct mr_gguf mr_gguf;
 
 /* ---- context, errors, streams -------------------------------------------- */
 /* Replaces candle's Device::new_metal(0) handle (engine.rs:278-298). */
@@ -204,6 +205,65 @@ int mr_moe_forward_residual(mr_ctx* ctx, const mr_layer* layer, const float* h, 
  * Replaces the multi-token paths layer.rs:1449-1514 and 2148-2183. */
 int mr_moe_forward_batched(mr_ctx* ctx, const mr_layer* layer, const float* x,
                            uint32_t n_tokens, float* y);
+
+/* ---- GGUF files (gguf/reader.rs; preload of engine.rs:1079-1255) ----------------- */
+/* Opens and memory-maps a GGUF v2/v3 file and parses its header, metadata and
+ * tensor index (GgufReader::open, reader.rs:259-358: the same magic/version
+ * checks, count limits, general.alignment (default 32) for the data start).
+ * Errors: MR_E_INVAL for a malformed or truncated file (message in
+ * mr_last_error(NULL)), MR_E_UNSUPPORTED for a tensor type outside
+ * GgmlQuantType (reader.rs:39-86). Host only: no context needed. */
+int mr_gguf_open(const char* path, mr_gguf** out);
+void mr_gguf_close(mr_gguf* g);
+uint64_t mr_gguf_n_tensors(const mr_gguf* g);
+/* Name of tensor i (index order of the file), NULL past the end. */
+const char* mr_gguf_tensor_name(const mr_gguf* g, uint64_t i);
+/* One tensor's TensorInfo (reader.rs:131-154): ggml type, dims in GGUF order
+ * (innermost first; pt_shape is the reverse), absolute data offset and raw byte
+ * size (raw_size, reader.rs:114-127). dims has room for 4 entries. */
+typedef struct mr_gguf_tensor {
+  uint32_t ggml_type;
+  uint32_t n_dims;
+  uint64_t dims[4];
+  uint64_t data_offset;
+  uint64_t nbytes;
+} mr_gguf_tensor;
+int mr_gguf_tensor_info(const mr_gguf* g, const char* name, mr_gguf_tensor* out);
+/* Read-only view of a tensor's bytes in the mapping (tensor_data, reader.rs:361-378;
+ * bounds-checked against the file size). Valid until mr_gguf_close. */
+int mr_gguf_tensor_data(const mr_gguf* g, const char* name, const void** data, uint64_t* nbytes);
+/* Metadata lookups (get_metadata + MetadataValue::as_u32 / as_f32 / as_str,
+ * reader.rs:170-218): MR_E_INVAL when the key is absent or of another type. */
+int mr_gguf_meta_u32(const mr_gguf* g, const char* key, uint32_t* out);
+int mr_gguf_meta_f32(const mr_gguf* g, const char* key, float* out);
+/* The string's bytes (not NUL-terminated) and length; valid until mr_gguf_close. */
+int mr_gguf_meta_str(const mr_gguf* g, const char* key, const char** str, uint64_t* len);
+/* Element count and, if out != NULL, up to cap elements of an integer array
+ * (as_u32_array, e.g. {arch}.experts_per_layer). */
+int mr_gguf_meta_u32_array(const mr_gguf* g, const char* key, uint32_t* out, uint64_t cap, uint64_t* n);
+/* Uploads a stacked expert tensor [E, out, in] (GGUF dims [in, out, E]) of
+ * MXFP4 or Q4_K in its native bytes: expert e at e * bytes_per_expert
+ * (expert_slice_data, reader.rs:394-444). */
+int mr_gguf_upload_experts(mr_ctx* ctx, const mr_gguf* g, const char* name, mr_pack** out);
+/* Options of mr_gguf_layer_create. */
+typedef struct mr_gguf_layer_opts {
+  uint32_t top_k;        /* 0: {arch}.expert_used_count */
+  int32_t route_flags;   /* -1: from the architecture (gpt-oss: softmax after top-k; else renormalised
+                            top-k, plain for general.name with Qwen1.5/Qwen2, config.rs:364) */
+  int32_t act;           /* -1: MR_ACT_SWIGLU_OAI for gpt-oss, else MR_ACT_SILU */
+  float alpha, limit;    /* OAI SwiGLU constants (layer.rs:873-874; 0: 1.702 and 7.0) */
+} mr_gguf_layer_opts;
+/* Builds MoE layer `layer` (tensors blk.<layer>.ffn_{gate,up,down}_exps.weight and
+ * their .bias, ffn_gate_inp.weight/.bias, the shared expert ffn_{gate,up,down}_shexp
+ * and ffn_gate_inp_shexp when present) on the device: experts uploaded natively,
+ * f32/f16/bf16 vectors converted to f32 (load_weight). The layer owns what it
+ * uploaded (freed by mr_layer_destroy). opts NULL: all defaults. The file can be
+ * closed afterwards. Also returns the layer's post_attention_norm weight as
+ * device f32 [H] in *norm_w (owned by the layer; NULL if the file has none) and
+ * {arch}.attention.layer_norm_rms_epsilon in *eps (default 1e-6, config.rs:293),
+ * for mr_moe_forward_residual; both outputs may be NULL. */
+int mr_gguf_layer_create(mr_ctx* ctx, const mr_gguf* g, uint32_t layer, const mr_gguf_layer_opts* opts,
+                         mr_layer** out, const float** norm_w, float* eps);
 
 /* ---- graph capture of a sequence of calls (no reference counterpart: the
  * reference's Metal command buffer batching, metal/mod.rs:6-14) ----------- */

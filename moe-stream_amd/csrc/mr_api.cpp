@@ -546,8 +546,11 @@ void mr_layer_destroy(mr_layer* L) {
     (void)hipStreamSynchronize(L->ctx->stream);
     (void)hipFree(L->fused_sync);
   }
+  for (mr_pack* p : L->own_packs) mr_pack_destroy(p);
+  for (void* d : L->own_dev) (void)mr_dev_free(L->ctx, d);
   delete L;
 }
+
 
 int mr_reserve(mr_ctx* c, const mr_layer* L, uint32_t max_tokens) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
@@ -807,3 +810,11 @@ int mr_synth_blocks(mr_ctx* c, int type, void* dst, uint64_t n_blocks, uint64_t 
 }
 
 }  // extern "C"
+
+namespace mr {
+int set_error(mr_ctx* ctx, int code, const char* msg) { return set_err(ctx, code, "%s", msg ? msg : ""); }
+void layer_adopt(mr_layer* L, mr_pack* const* packs, size_t n_packs, void* const* dev, size_t n_dev) {
+  L->own_packs.insert(L->own_packs.end(), packs, packs + n_packs);
+  L->own_dev.insert(L->own_dev.end(), dev, dev + n_dev);
+}
+}  // namespace mr

@@ -115,6 +115,8 @@ struct mr_layer {
   int type = 0;
   uint32_t* fused_sync = nullptr;  // device sync block of the fused decode kernel
   const mr_layer* next = nullptr;  // layer run after this one (router prefetch hint) or NULL
+  std::vector<mr_pack*> own_packs;  // device objects the layer owns (mr_gguf_layer_create)
+  std::vector<void*> own_dev;
 };
 
 struct mr_graph {
@@ -138,6 +140,11 @@ hipError_t launch_rms_norm(const Launch& K, const float* h, const float* w, floa
                            float* out);
 hipError_t launch_residual_add(const Launch& K, const float* h, const float* m, uint64_t n, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+
+// Records an error on the context (or the calling thread when ctx is NULL); returns code.
+int set_error(mr_ctx* ctx, int code, const char* msg);
+// Hands packs and device buffers to a layer, which frees them in mr_layer_destroy.
+void layer_adopt(mr_layer* L, mr_pack* const* packs, size_t n_packs, void* const* dev, size_t n_dev);
 
 // Fused RMSNorm of the layer input and residual added to its output
 // (mr_moe_forward_residual; norm.rs:16-37, layer.rs:462-473). w == nullptr: off.

@@ -40,6 +40,16 @@ _lib = C.CDLL(str(LIB_PATH))
 _vp, _u32, _u64, _i32, _f32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int32, C.c_float
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [("ggml_type", C.c_uint32), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("data_offset", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
+class GgufLayerOpts(C.Structure):
+    _fields_ = [("top_k", C.c_uint32), ("route_flags", C.c_int32), ("act", C.c_int32),
+                ("alpha", C.c_float), ("limit", C.c_float)]
+
+
 class LayerDesc(C.Structure):
     _fields_ = [
         ("gate", _vp), ("up", _vp), ("down", _vp),
@@ -81,6 +91,19 @@ _SIGS = {
     "mr_moe_forward": (C.c_int, [_vp, _vp, _vp, _vp]),
     "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
+    "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "mr_gguf_close": (None, [_vp]),
+    "mr_gguf_n_tensors": (_u64, [_vp]),
+    "mr_gguf_tensor_name": (C.c_char_p, [_vp, _u64]),
+    "mr_gguf_tensor_info": (C.c_int, [_vp, C.c_char_p, C.POINTER(GgufTensor)]),
+    "mr_gguf_tensor_data": (C.c_int, [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(_u64)]),
+    "mr_gguf_meta_u32": (C.c_int, [_vp, C.c_char_p, C.POINTER(_u32)]),
+    "mr_gguf_meta_f32": (C.c_int, [_vp, C.c_char_p, C.POINTER(_f32)]),
+    "mr_gguf_meta_str": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(_u64)]),
+    "mr_gguf_meta_u32_array": (C.c_int, [_vp, C.c_char_p, _vp, _u64, C.POINTER(_u64)]),
+    "mr_gguf_upload_experts": (C.c_int, [_vp, _vp, C.c_char_p, C.POINTER(_vp)]),
+    "mr_gguf_layer_create": (C.c_int, [_vp, _vp, _u32, C.POINTER(GgufLayerOpts), C.POINTER(_vp),
+                                       C.POINTER(_vp), C.POINTER(_f32)]),
     "mr_graph_begin": (C.c_int, [_vp]),
     "mr_graph_end": (C.c_int, [_vp, C.POINTER(_vp)]),
     "mr_graph_launch": (C.c_int, [_vp, _vp]),
@@ -342,6 +365,84 @@ class MoeLayer:
             _lib.mr_layer_destroy(self.h)
             self.h = None
             self._next = None
+
+
+def _gguf_check(rc: int) -> None:
+    if rc != MR_OK:
+        raise MoeRocmError(rc, _lib.mr_last_error(None).decode(errors="replace"))
+
+
+class GgufFile:
+    """A memory-mapped GGUF file (mr_gguf_open; GgufReader, gguf/reader.rs)."""
+
+    def __init__(self, path):
+        h = _vp()
+        _gguf_check(_lib.mr_gguf_open(str(path).encode(), C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            _lib.mr_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def tensor_names(self) -> list[str]:
+        n = _lib.mr_gguf_n_tensors(self.h)
+        return [_lib.mr_gguf_tensor_name(self.h, i).decode() for i in range(n)]
+
+    def info(self, name: str) -> dict:
+        t = GgufTensor()
+        _gguf_check(_lib.mr_gguf_tensor_info(self.h, name.encode(), C.byref(t)))
+        return dict(ggml_type=t.ggml_type, dims=tuple(t.dims[: t.n_dims]), data_offset=t.data_offset,
+                    nbytes=t.nbytes)
+
+    def data(self, name: str) -> np.ndarray:
+        p, n = _vp(), _u64()
+        _gguf_check(_lib.mr_gguf_tensor_data(self.h, name.encode(), C.byref(p), C.byref(n)))
+        return np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p.value)).copy()
+
+    def meta_u32(self, key: str) -> int:
+        v = _u32()
+        _gguf_check(_lib.mr_gguf_meta_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_f32(self, key: str) -> float:
+        v = _f32()
+        _gguf_check(_lib.mr_gguf_meta_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_str(self, key: str) -> str:
+        p, n = C.c_void_p(), _u64()
+        _gguf_check(_lib.mr_gguf_meta_str(self.h, key.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p.value, n.value).decode() if n.value else ""
+
+    def meta_u32_array(self, key: str) -> list[int]:
+        n = _u64()
+        _gguf_check(_lib.mr_gguf_meta_u32_array(self.h, key.encode(), None, 0, C.byref(n)))
+        out = np.zeros(n.value, dtype=np.uint32)
+        _gguf_check(_lib.mr_gguf_meta_u32_array(self.h, key.encode(), out.ctypes.data, n.value, C.byref(n)))
+        return out.tolist()
+
+    def layer(self, ctx: "Context", index: int, *, top_k: int = 0, route_flags: int = -1, act: int = -1,
+              alpha: float = 0.0, limit: float = 0.0) -> "MoeLayer":
+        """mr_gguf_layer_create: the MoE layer `index`, owning its device copies; the
+        returned layer's `norm_w` (device pointer or None) and `eps` feed forward_residual."""
+        o = GgufLayerOpts(top_k=top_k, route_flags=route_flags, act=act, alpha=alpha, limit=limit)
+        h, nw, eps = _vp(), _vp(), _f32()
+        ctx.check(_lib.mr_gguf_layer_create(ctx.h, self.h, index, C.byref(o), C.byref(h), C.byref(nw),
+                                            C.byref(eps)))
+        L = MoeLayer.__new__(MoeLayer)
+        L.ctx, L.h, L.desc, L._refs, L._next = ctx, h.value, None, (), None
+        gate = self.info(f"blk.{index}.ffn_gate_exps.weight")
+        L.hidden, L.inter, L.n_experts = gate["dims"][0], gate["dims"][1], gate["dims"][2]
+        L.top_k = top_k or self.meta_u32(f"{self.meta_str('general.architecture')}.expert_used_count")
+        L.norm_w, L.eps = nw.value, eps.value
+        return L
 
 
 def topk(ctx: Context, logits, n_tokens: int, n_experts: int, top_k: int, flags: int, idx, w) -> None:
