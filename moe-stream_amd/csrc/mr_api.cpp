@@ -519,8 +519,8 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
     // sync block of the fused decode kernel: counters start at zero
     int rc = bind(c);
     void* fs = nullptr;
-    hipError_t e = rc ? hipSuccess : hipMalloc(&fs, mr::fused_layer_sync_bytes());
-    if (!rc && e == hipSuccess) e = hipMemset(fs, 0, mr::fused_layer_sync_bytes());
+    hipError_t e = rc ? hipSuccess : hipMalloc(&fs, mr::fused_layer_sync_bytes(*L));
+    if (!rc && e == hipSuccess) e = hipMemset(fs, 0, mr::fused_layer_sync_bytes(*L));
     if (rc || e != hipSuccess) {
       if (fs) (void)hipFree(fs);
       delete L;

@@ -624,7 +624,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 }
 
 // Shapes the fused kernel runs; others take the VALU path.
-uint64_t fused_layer_sync_bytes() { return (uint64_t)kLayerSyncWords * 4; }
+uint64_t fused_layer_sync_bytes(const mr_layer& L) { return layer_sync_words(L.E + (L.d.sh_gate ? 1u : 0u)) * 4; }
 
 bool fused_supported(const mr_layer& L, int n_cu) {
   if (L.type != MR_GGML_MXFP4 || L.d.sh_gate || L.d.top_k > 4) return false;

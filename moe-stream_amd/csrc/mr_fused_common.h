@@ -31,7 +31,10 @@ enum : int {
   FS_LOGITS = FS_WGSEQ + kMaxGrid              // [kLogitCopies][n_logits] (logit bits, launch flag)
                                                // word pairs: E experts, then extras
 };
-constexpr int kLayerSyncWords = FS_LOGITS + kLogitCopies * 2 * kMaxLogits;
+// The block's size for n_logits published logits (logit_copy's stride times the copies).
+inline uint64_t layer_sync_words(uint32_t n_logits) {
+  return (uint64_t)FS_LOGITS + (uint64_t)kLogitCopies * ((2u * n_logits + 31u) & ~31u);
+}
 
 // Launch sequence number of this layer's kernel. Every launch of a layer runs
 // the same grid, so each workgroup keeps its own count (read at entry, stored

@@ -160,7 +160,7 @@ bool fused_supported(const mr_layer& L, int n_cu);
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
                         const NormResid& nr = NormResid{});
-uint64_t fused_layer_sync_bytes();
+uint64_t fused_layer_sync_bytes(const mr_layer& L);  // sync block of one layer (its logit count)
 
 // Scratch of the grouped multi-token MXFP4 path (device pointers; P = T * top_k pairs).
 struct GroupedScratch {
