@@ -165,14 +165,17 @@ __device__ __forceinline__ void issue_rows(const uint8_t* W, int S, int nb, int 
   }
 }
 
-// ---- gate/up weight stream through LDS --------------------------------------------------------
+// ---- gate/up weight stream -------------------------------------------------------------------
 // A wave's 16-row tile (rows adjacent in memory, rb bytes apart) is streamed in chunks of
 // kStreamSteps K steps = 4*kStreamSteps blocks: each row's chunk is fetched as kRowPieces
-// 16-byte pieces from the 16-byte aligned address at or below its first byte, by direct
-// global->LDS loads whose LDS destination is piece index * 16 (lane-contiguous), so one wave
-// load covers about four rows' contiguous bytes instead of sixteen scattered windows. The
-// MFMA A windows are read back from LDS. Two buffers per wave: chunk c+1 streams in while
-// chunk c is multiplied.
+// 16-byte pieces from the 16-byte aligned address at or below its first byte, lane-contiguous,
+// so one wave load covers about four rows' contiguous bytes instead of sixteen scattered
+// windows. kChunkAhead chunks beyond the one being multiplied are in flight in VGPRs (16 each);
+// a landed chunk is written to the wave's LDS buffer (piece index * 16) and the MFMA A windows
+// are read back from there (two buffers, alternating). The code is straight-line over the
+// kMaxChunks chunks with one uniform branch per chunk, which keeps each chunk's MFMAs next to
+// their operands; chunks past the row end load clamped pieces and multiply the zero B line, so
+// every path issues the same loads and the compiler's own vmcnt waits stay exact.
 constexpr int kStreamSteps = 3;
 constexpr int kRowPieces = 15;                    // row slot: 240 bytes
 constexpr int kStageLoads = 4;                    // wave loads per chunk (64 pieces each)
@@ -184,84 +187,7 @@ static_assert(15 + 17 * 4 * kStreamSteps + 3 <= 16 * kRowPieces, "a row slot hol
 static_assert(kStageOff + 4 * 2 * kStageBytes <= 4 * kImgVec * 1024, "stage buffers fit the dynamic LDS");
 static_assert(4 * kSteps * kImgBytes <= kImgVec * 1024 && 4 * kSteps <= 128, "a down slot image holds 4*kSteps blocks");
 
-__device__ __forceinline__ void stream_issue(const uint8_t* W, uint64_t rb, int nb, int c, uint8_t* buf,
-                                             int lane) {
-  const int b0 = 4 * kStreamSteps * c;
-#pragma unroll
-  for (int it = 0; it < kStageLoads; ++it) {
-    const int q = it * 64 + lane;
-    const int row = min(q / kRowPieces, 15);
-    const int pc = min(q - row * kRowPieces, kRowPieces - 1);
-    const uint8_t* rs = W + (uint64_t)row * rb;
-    const uintptr_t first = reinterpret_cast<uintptr_t>(rs + (size_t)b0 * 17) & ~(uintptr_t)15;
-    const uintptr_t last = (reinterpret_cast<uintptr_t>(rs + (size_t)nb * 17) - 1) & ~(uintptr_t)15;
-    const uintptr_t src = min(first + 16 * (uintptr_t)pc, last);  // never past the row's last piece
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), buf + it * 1024, 16, 0, 0);
-  }
-}
-
-// D of one 16-row tile over all K steps: A streamed through `stage` (two kStageBytes buffers
-// of this wave), B from an x image in LDS. W: row 0 of the tile.
-__device__ __forceinline__ f32x4 stream_chain(const uint8_t* W, uint64_t rb, int S, int nb, uint8_t* stage,
-                                              const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
-                                              int lane, int i, int g) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd steps
-  const int nc = (S + kStreamSteps - 1) / kStreamSteps;
-  const uintptr_t rs = reinterpret_cast<uintptr_t>(W + (uint64_t)i * rb);  // this lane's row
-  stream_issue(W, rb, nb, 0, stage, lane);
-#pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    if (c < nc) {
-      if (c + 1 < nc) {
-        stream_issue(W, rb, nb, c + 1, stage + ((c + 1) & 1) * kStageBytes, lane);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStageLoads) : "memory");  // chunk c has landed
-      } else {
-        vm_drain();
-      }
-      __builtin_amdgcn_wave_barrier();
-      const uint8_t* buf = stage + (c & 1) * kStageBytes;
-      const int b0 = 4 * kStreamSteps * c;
-      const int lead = (int)((rs + (uintptr_t)b0 * 17) & 15u);  // row chunk start within its first piece
-      // all kStreamSteps steps, unguarded: steps past S read the zero B line and add 0
-      RawBlk r[kStreamSteps];
-      i32x8 B[kStreamSteps];
-      int sb[kStreamSteps], off[kStreamSteps];
-#pragma unroll
-      for (int s = 0; s < kStreamSteps; ++s) {  // every operand of the chunk is loaded first
-        const int st = kStreamSteps * c + s;
-        const int b = 4 * st + g;
-        off[s] = i * (kRowPieces * 16) + lead + (b - b0) * 17;
-        const uint32_t* wp = reinterpret_cast<const uint32_t*>(buf + (off[s] & ~3));
-        r[s].d[0] = wp[0], r[s].d[1] = wp[1], r[s].d[2] = wp[2], r[s].d[3] = wp[3], r[s].d[4] = wp[4];
-        load_b(img, sc, zero, st, nb, i, g, B[s], sb[s]);
-      }
-#pragma unroll
-      for (int s = 0; s < kStreamSteps; ++s) {
-        const int st = kStreamSteps * c + s;
-        const int b = 4 * st + g;
-        if (st & 1)
-          acc1 = mfma_raw(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc1);
-        else
-          acc = mfma_raw(r[s], (uint32_t)off[s] & 3u, b < nb, B[s], sb[s], acc);
-      }
-      lds_drain();  // this buffer is refilled by the next iteration's stream_issue
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-  return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
-}
-
-// The same chunk stream with the chunks held in VGPRs while they are in flight: kChunkAhead
-// chunks beyond the one being multiplied are requested (16 VGPRs each), so a wave keeps
-// (kChunkAhead + 1) x 4 KB of loads outstanding instead of the one chunk two LDS buffers
-// allow. A landed chunk is written to this wave's LDS buffer (same layout as stream_issue
-// produces) and the MFMA windows are read back from there. The code is straight-line over
-// kMaxChunks chunks: chunks past the row end load clamped pieces and multiply the zero B
-// line, so the compiler's own vmcnt waits stay exact.
-#ifndef MR_CHUNK_AHEAD
-#define MR_CHUNK_AHEAD 2
-#endif
-constexpr int kChunkAhead = MR_CHUNK_AHEAD;
+constexpr int kChunkAhead = 2;  // measured: 1-4 within 1%, 2 best
 
 // Per-lane piece geometry of a 16-row tile, as byte offsets from the tile's first row (W):
 // lane piece q = it*64 + lane is piece pc of row `row`; rowa = (W & 15) + row*rb is the row's
@@ -294,9 +220,11 @@ __device__ __forceinline__ void piece_fetch(const uint8_t* Wa, const PieceMap& m
   }
 }
 
+// after_issue() runs once the first chunks' loads are in flight (work that can wait for them).
+template <typename F>
 __device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, int nb, uint8_t* stage,
                                                 const uint8_t* img, const uint32_t* sc, const uint8_t* zero,
-                                                int lane, int i, int g) {
+                                                int lane, int i, int g, F&& after_issue) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd steps
   const uint8_t* Wa = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(W) & ~(uintptr_t)15);
   const PieceMap m = piece_map(W, rb, nb, lane);
@@ -306,6 +234,7 @@ __device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, i
   i32x4 v[kMaxChunks][kStageLoads];
 #pragma unroll
   for (int c = 0; c < kChunkAhead && c < kMaxChunks; ++c) piece_fetch(Wa, m, c, v[c]);
+  after_issue();
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
     // The branch on c < nc (wave-uniform) also closes a basic block per chunk, which keeps
@@ -461,17 +390,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     }
     TRACE(1);
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+    RouteState rs;  // wave 0: the selection, finished (weights, order) once its stream is issued
+    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     XTRACE(wave);  // per wave: at the routing barrier
-    __syncthreads();  // routing and x image ready
+    __syncthreads();  // selection and x image ready
     TRACE(2);
     if (ok_flag && gid < a.NG) {  // one unit per workgroup
       const int unit = gid;
       const int slot = unit / nrp, pair = unit % nrp;
       const int e = sel_i[slot];
-      const float wsl = sel_w[slot];
       const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
       const int S = (nbH + 3) >> 2;
       const uint64_t rb = (uint64_t)nbH * 17;
@@ -483,14 +412,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         if (a.gate_b) gbias = a.gate_b[bi];
         if (a.up_b) ubias = a.up_b[bi];
       }
-#if MR_CHUNK_AHEAD > 0
       (void)S;
       f32x4 dacc = stream_chain_v(W, (uint32_t)rb, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
-                                  lds_zero, lane, i, g);
-#else
-      f32x4 dacc = stream_chain(W, rb, S, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
-                                lds_zero, lane, i, g);
-#endif
+                                  lds_zero, lane, i, g, [&] {
+                                    if (wave == 0) route_finish(rc, rs, sel_w, sel_o);
+                                  });
       XTRACE(4 + wave);  // per wave: chain done
       TRACE(3);
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
@@ -508,7 +434,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           if (a.gate_b) gv = gv + gbias;
           if (a.up_b) uv = uv + ubias;
           const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-          lds_act[lane] = h * wsl;
+          lds_act[lane] = h * sel_w[slot];  // written by this wave's route_finish
         }
         __builtin_amdgcn_wave_barrier();
         if (lane < 8) {  // split the 32 values: one 32-element block of the down input
@@ -532,7 +458,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     // ------------------------------------------------------------- down
     const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
-    if (wave == 0 && !route_wave(rc, seq, sel_i, sel_w, sel_o)) {
+    RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
+    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();
@@ -546,10 +473,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       int slot = wave;
       const uint8_t* D = a.down + a.down_off[sel_i[slot < a.k ? slot : 0]] + (uint64_t)row * rb;
       if (slot < a.k) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
+      if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
-      int so[4];
+      int so[4] = {0, 0, 0, 0};
+      if (wave == 0) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) so[p] = sel_o[min(p, a.k - 1)] * 16;
+        for (int p = 0; p < 4; ++p) so[p] = sel_o[min(p, a.k - 1)] * 16;
+      }
       // this thread's output-row bias terms and residual, also independent of gate/up
       const float yres = (tid < 16 && NORM && q * 16 + tid < a.H) ? a.nr.resid[q * 16 + tid] : 0.f;
       float ybias = 0.f;

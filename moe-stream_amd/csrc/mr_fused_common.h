@@ -313,7 +313,14 @@ __device__ __forceinline__ void cas_desc(uint32_t& ka, int& ia, uint32_t& kb, in
 // wave-wide largest head (DPP max; ties: the lowest expert index) and pop it.
 // Writes slot -> (expert, weight) and ord[p] = the slot holding the p-th
 // smallest expert index (the combine order of layer.rs:1092-1106).
-__device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, float* sel_w, int* ord) {
+// Selection part: poll the logits and pick the k experts; slot r's expert goes to sel_i[r]
+// (LDS) and, for route_finish, stays in the state (lane r = slot r).
+struct RouteState {
+  float v[kRouteVals];  // this lane's logits
+  uint32_t my_key;
+  int my_e;
+};
+__device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, RouteState& st) {
   const int lane = threadIdx.x & 63;
   RTRACE(0);
   const int nj = (rc.E + 63) >> 6;  // values per lane (wave-uniform)
@@ -346,20 +353,6 @@ __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, 
   // same probability (a tie by value, which the tests treat as ambiguous).
   // Weights: GPT-OSS (softmax over the k) and renormalised Qwen routing are the same
   // softmax over the k selected logits; plain Qwen routing needs the all-expert sum.
-  const bool sel_softmax = (rc.flags & (MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK)) != 0u;
-  float m_all = 0.f, s_all = 1.f;
-  if (!sel_softmax) {
-    RTRACE(2);
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j) m = fmaxf(m, v[j]);
-    m_all = wave_max_f(m);
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j)
-      if (lane + 64 * j < rc.E) s += __expf(v[j] - m_all);
-    s_all = wave_sum_f(s);
-  }
   RTRACE(3);
   uint32_t key[kRouteVals];
   int idx[kRouteVals];
@@ -398,9 +391,38 @@ __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, 
     }
   }
   RTRACE(5);
-  // weights over the k selected logits (lane r = slot r, in selection order)
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) st.v[j] = v[j];
+  st.my_key = my_key, st.my_e = my_e;
+  if (lane < rc.k) sel_i[lane] = my_e;
+  lds_drain();
+  RTRACE(7);
+  return true;
+}
+
+
+// Weights and combine order of the selection (the top-k weights of top_k_routing,
+// layer.rs:2346-2403; ascending expert order, layer.rs:1092-1106): sel_w[r] for slot r, and
+// ord[p] = the slot holding the p-th smallest expert index. Not needed to start streaming
+// weights, so callers run it after their first loads are issued.
+__device__ inline void route_finish(const RouteCfg& rc, const RouteState& st, float* sel_w, int* ord) {
+  const int lane = threadIdx.x & 63;
+  const float* v = st.v;
+  const bool sel_softmax = (rc.flags & (MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK)) != 0u;
+  float m_all = 0.f, s_all = 1.f;  // plain softmax: the all-expert normaliser
+  if (!sel_softmax) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j) m = fmaxf(m, v[j]);
+    m_all = wave_max_f(m);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j)
+      if (lane + 64 * j < rc.E) s += __expf(v[j] - m_all);
+    s_all = wave_sum_f(s);
+  }
   const bool in = lane < rc.k;
-  const float l = in ? key_value(my_key) : 0.f;
+  const float l = in ? key_value(st.my_key) : 0.f;
   float w;
   if (sel_softmax) {
     const float m = lane_f<0>(l);  // slot 0 holds the largest logit
@@ -412,10 +434,16 @@ __device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, 
   int p = 0;  // position of this slot's expert in ascending expert order
 #pragma unroll
   for (int r = 0; r < 16; ++r)
-    if (r < rc.k) p += __builtin_amdgcn_readlane(my_e, r) < my_e ? 1 : 0;
-  if (in) sel_i[lane] = my_e, sel_w[lane] = w, ord[p] = lane;
+    if (r < rc.k) p += __builtin_amdgcn_readlane(st.my_e, r) < st.my_e ? 1 : 0;
+  if (in) sel_w[lane] = w, ord[p] = lane;
   lds_drain();
-  RTRACE(7);
+}
+
+// Both parts in one call.
+__device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, float* sel_w, int* ord) {
+  RouteState st;
+  if (!route_select(rc, seq, sel_i, st)) return false;
+  route_finish(rc, st, sel_w, ord);
   return true;
 }
 
