@@ -348,15 +348,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     }
     TRACE(1);
     if (tid == 0) ok_flag = 1;
-    if (wave == 0) {
-      if (!route_wave(rc, seq, sel_i, sel_w, sel_o)) {
-        if (lane == 0) ok_flag = 0, fail(a.err);
-      } else if (a.has_sh && lane == 0) {
-        const float z = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
-        sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(z) : 1.f;
-      }
+    RouteState rs;  // wave 0: the selection, finished (weights, order) once its loads are issued
+    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+      if (lane == 0) ok_flag = 0, fail(a.err);
     }
-    __syncthreads();  // routing and the x image ready
+    __syncthreads();  // selection and the x image ready
     TRACE(2);
     if (ok_flag) {
       const int slot = gid / nGI, urow = gid - slot * nGI;
@@ -367,6 +363,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const size_t rb = (size_t)nsbH * 144;
       uint4 ch[1][kQ4GuIt];
       region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
+      if (wave == 0) {  // routing weights (and the shared expert's sigmoid gate) while the rows load
+        route_finish(rc, rs, sel_w, sel_o);
+        if (a.has_sh && lane == 0) {
+          const float z = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
+          sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(z) : 1.f;
+        }
+      }
       // the epilogue's biases (wave 0, lanes < 16), loaded before the dot products
       float gbias = 0.f, ubias = 0.f;
       if (wave == 0 && lane < 16 && !sh) {
@@ -416,10 +419,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     // ------------------------------------------------------------- down
     const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
-    if (wave == 0) {
-      if (!route_wave(rc, seq, sel_i, sel_w, sel_o)) {
-        if (lane == 0) ok_flag = 0, fail(a.err);
-      }
+    RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
+    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+      if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();
     TRACE(1);
@@ -433,6 +435,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         const uint8_t* D = sc >= a.k ? a.sh_down : a.down + a.down_off[sel_i[sc]];
         if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, nsbI, ch[j]);
       }
+      if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       const float yres = (tid < 8 && NORM && q * 8 + tid < a.H) ? a.nr.resid[q * 8 + tid] : 0.f;
       float ybias = 0.f;  // this row's routed bias terms (layer.rs:1417-1444)
       if (tid < 8 && a.down_b)
