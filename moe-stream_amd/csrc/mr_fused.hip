@@ -79,6 +79,7 @@ struct FusedArgs {
   int act;
   float alpha, limit;
   int R, NG, ND;
+  int NS;  // down row groups split into two 8-row workgroups (CU balance)
   uint32_t spin_limit;
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     }
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, lds_dyn);
-  } else if (bid >= a.R + a.ND) {
+  } else if (bid >= a.R + a.ND && bid < a.R + a.ND + a.NG) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
     const int nrp = a.I >> 5;
@@ -456,7 +457,12 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     if (tid == 0) count(a.fs + FS_GU, gid);
   } else {
     // ------------------------------------------------------------- down
-    const int q = bid - a.R;
+    // Row group q of 16 output rows. The first NS groups are split: rows 0-7 here, rows
+    // 8-15 in a workgroup after the gate/up range (half 2). A half's idle lanes read the
+    // row of their partner lane (i ^ 8): the same addresses, so no extra HBM bytes.
+    const int tail = bid - (a.R + a.ND + a.NG);
+    const int q = tail >= 0 ? tail : bid - a.R;
+    const int half = tail >= 0 ? 2 : (q < a.NS ? 1 : 0);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
     if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
@@ -466,7 +472,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     TRACE(1);
     if (ok_flag) {
       const int S = (nbI + 3) >> 2;
-      const int row = q * 16 + i;
+      const int row = q * 16 + (half == 0 ? i : (half == 2 ? 8 : 0) + (i & 7));
       const uint64_t rb = (uint64_t)nbI * 17;
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
       RawBlk rd[kSteps];
@@ -530,7 +536,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           if (i == 0) lds_part[wave * 16 + 4 * g + r] = s;
         }
         __syncthreads();
-        if (tid < 16) {
+        if (tid < 16 && (half == 0 || (tid >> 3) == half - 1)) {
           const int rr = q * 16 + tid;
           float yv = 0.f;  // slots in ascending expert order (layer.rs:1092-1106)
 #pragma unroll
@@ -560,7 +566,7 @@ bool fused_supported(const mr_layer& L, int n_cu) {
   if (L.type != MR_GGML_MXFP4 || L.d.sh_gate || L.d.top_k > 4) return false;
   const uint64_t R = (L.E + 3) / 4, ND = (L.H + 15) / 16, NG = (uint64_t)L.d.top_k * (L.I / 32);
   if (R + ND >= (uint64_t)n_cu || R + ND + NG > 3ull * n_cu) return false;  // one dispatch round
-  if (R + ND + NG > (uint64_t)kMaxGrid) return false;
+  if (R + ND + NG > (uint64_t)kMaxGrid) return false;  // the split groups are added only where they fit
   const uint64_t nbH = L.H / 32, nbI = L.I / 32;
   if ((nbH + 3) / 4 > (uint64_t)kSteps || (nbI + 3) / 4 > (uint64_t)kSteps) return false;
   if (nbH > 96 || nbI * kImgBytes > (uint64_t)kImgVec * 64 * 16 || nbI > 128) return false;
@@ -593,6 +599,12 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.R = (int)((L.E + 3) / 4);
   a.NG = (int)(k * nbI);
   a.ND = (int)((L.H + 15) / 16);
+  // Workgroups go to CUs round robin (workgroup b on CU b mod n_cu, three per CU). With
+  // more than 2 n_cu down and gate/up units, the CUs of the third round that also hold a
+  // down group carry three units; splitting those down groups in halves, the second half
+  // in a third-round slot on a CU with two units, caps every CU at 2.5 units.
+  const int grid0 = a.R + a.ND + a.NG;
+  a.NS = std::max(0, std::min({a.ND + a.NG - 2 * n_cu, a.ND, 3 * n_cu - grid0, kMaxGrid - grid0}));
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
@@ -603,9 +615,9 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   const size_t lds = img_bytes + sc_words * 4;
   ProfScope ps(K, "fused_layer");
   if (nr.w)
-    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
+    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(grid0 + a.NS), dim3(256), lds, K.s, a);
   else
-    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(a.R + a.ND + a.NG), dim3(256), lds, K.s, a);
+    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(grid0 + a.NS), dim3(256), lds, K.s, a);
   return hipGetLastError();
 }
 
