@@ -84,6 +84,11 @@ int pack_common(mr_ctx* c, int type, const void* bytes, uint64_t nbytes, uint32_
   p->nbytes = nbytes;
   p->matrix_bytes = mb;
   p->h_offsets = std::move(off);
+  p->uniform = true;
+  p->uni_off0 = p->h_offsets[0];
+  p->uni_stride = E > 1 ? p->h_offsets[1] - p->h_offsets[0] : 0;
+  for (uint32_t e = 1; e < E && p->uniform; ++e)
+    p->uniform = p->h_offsets[e] >= p->uni_off0 && p->h_offsets[e] - p->uni_off0 == (uint64_t)e * p->uni_stride;
   *res = p;
   return MR_OK;
 }

@@ -56,12 +56,7 @@ constexpr int kImgVec = 12;             // 16-byte image loads per lane for one 
 
 
 struct FusedArgs {
-  const uint8_t* gate;
-  const uint8_t* up;
-  const uint8_t* down;
-  const uint64_t* gate_off;
-  const uint64_t* up_off;
-  const uint64_t* down_off;
+  ExpertLoc gate, up, down;
   const float* gate_b;
   const float* up_b;
   const float* down_b;
@@ -405,7 +400,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
       const int S = (nbH + 3) >> 2;
       const uint64_t rb = (uint64_t)nbH * 17;
-      const uint8_t* W = (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]) + (uint64_t)(pair * 32 + tile * 16) * rb;
+      const uint8_t* W = expert_at(mat ? a.up : a.gate, e) + (uint64_t)(pair * 32 + tile * 16) * rb;
       // the epilogue's biases (wave 0, lanes < 32), loaded before the weight stream
       float gbias = 0.f, ubias = 0.f;
       if (wave == 0 && lane < 32) {
@@ -477,7 +472,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
       RawBlk rd[kSteps];
       int slot = wave;
-      const uint8_t* D = a.down + a.down_off[sel_i[slot < a.k ? slot : 0]] + (uint64_t)row * rb;
+      const uint8_t* D = expert_at(a.down, sel_i[slot < a.k ? slot : 0]) + (uint64_t)row * rb;
       if (slot < a.k) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
@@ -555,6 +550,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   TRACE(5);
 #ifdef MR_FUSED_TRACE
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
+  if (a.trace && (threadIdx.x & 63) == 0)  // HW_ID: wave, SIMD, CU, SE of each wave
+    a.trace[blockIdx.x * 32 + 26 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
   if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
 }
@@ -586,8 +583,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
 #ifdef MR_FUSED_TRACE
   a.trace = g_fused_trace;
 #endif
-  a.gate = L.d.gate->base, a.up = L.d.up->base, a.down = L.d.down->base;
-  a.gate_off = L.d.gate->d_offsets, a.up_off = L.d.up->d_offsets, a.down_off = L.d.down->d_offsets;
+  a.gate = expert_loc(L.d.gate), a.up = expert_loc(L.d.up), a.down = expert_loc(L.d.down);
   a.gate_b = L.d.gate_bias, a.up_b = L.d.up_bias, a.down_b = L.d.down_bias;
   a.router_w = L.d.router_w, a.router_b = L.d.router_b, a.mask = L.d.dummy_mask;
   a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;

@@ -41,6 +41,10 @@ inline uint64_t layer_sync_words(uint32_t n_logits) {
 // +1 at exit): all workgroups of a launch read the same value, with no atomic.
 __device__ __forceinline__ uint32_t* wg_seq_word(uint32_t* fs) { return fs + FS_WGSEQ + blockIdx.x; }
 
+__device__ __forceinline__ const uint8_t* expert_at(const ExpertLoc& l, int e) {
+  return l.base + (l.tab ? l.tab[e] : (uint64_t)e * l.stride);
+}
+
 #ifdef MR_FUSED_TRACE
 #define TRACE(slot)                                                                       \
   do {                                                                                    \

@@ -74,12 +74,7 @@ static_assert(72 * (kQ4MaxH / 256) <= 64 * kQ4GuIt && 72 * (kQ4MaxI / 256) <= 64
 static_assert(72 * (kQ4MaxH / 256) <= 576, "per-wave LDS slices hold a gate/up region");
 
 struct Q4Args {
-  const uint8_t* gate;
-  const uint8_t* up;
-  const uint8_t* down;
-  const uint64_t* gate_off;
-  const uint64_t* up_off;
-  const uint64_t* down_off;
+  ExpertLoc gate, up, down;
   const uint8_t* sh_gate;  // shared expert matrices (one expert) or null
   const uint8_t* sh_up;
   const uint8_t* sh_down;
@@ -359,7 +354,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const bool sh = slot >= a.k;
       const int mat = wave >> 1, half = wave & 1;
       const int e = sh ? 0 : sel_i[slot];
-      const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : (mat ? a.up + a.up_off[e] : a.gate + a.gate_off[e]);
+      const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e);
       const size_t rb = (size_t)nsbH * 144;
       uint4 ch[1][kQ4GuIt];
       region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
@@ -432,7 +427,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       for (int j = 0; j < kQ4DnSlots; ++j) {
         const int s = wave + 4 * j;
         const int sc = s < a.ktot ? s : 0;
-        const uint8_t* D = sc >= a.k ? a.sh_down : a.down + a.down_off[sel_i[sc]];
+        const uint8_t* D = sc >= a.k ? a.sh_down : expert_at(a.down, sel_i[sc]);
         if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, nsbI, ch[j]);
       }
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
@@ -502,6 +497,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   TRACE(5);
 #ifdef MR_FUSED_TRACE
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
+  if (a.trace && (threadIdx.x & 63) == 0)  // HW_ID: wave, SIMD, CU, SE of each wave
+    a.trace[blockIdx.x * 32 + 26 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
   if (tid == 0) st_sc1(wg_seq_word(a.fs), seq + 1u);
 }
@@ -530,8 +527,7 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
 #ifdef MR_FUSED_TRACE
   a.trace = g_fused_trace;
 #endif
-  a.gate = L.d.gate->base, a.up = L.d.up->base, a.down = L.d.down->base;
-  a.gate_off = L.d.gate->d_offsets, a.up_off = L.d.up->d_offsets, a.down_off = L.d.down->d_offsets;
+  a.gate = expert_loc(L.d.gate), a.up = expert_loc(L.d.up), a.down = expert_loc(L.d.down);
   a.has_sh = L.d.sh_gate ? 1 : 0;
   if (a.has_sh) {
     a.sh_gate = L.d.sh_gate->base + L.d.sh_gate->h_offsets[0];

@@ -106,7 +106,24 @@ struct mr_pack {
   uint64_t matrix_bytes = 0;       // bytes of one expert matrix
   std::vector<uint64_t> h_offsets; // per-expert byte offsets from base
   uint64_t* d_offsets = nullptr;   // same on the device (nullptr for host-only ctx)
+  bool uniform = false;            // h_offsets[e] == uni_off0 + e * uni_stride for every e
+  uint64_t uni_off0 = 0, uni_stride = 0;
 };
+
+namespace mr {
+// Where the fused kernels find expert e: base + e * stride when the pack's experts sit
+// one stride apart (no table read between the routing and the weight loads), else
+// base + tab[e].
+struct ExpertLoc {
+  const uint8_t* base;
+  const uint64_t* tab;  // nullptr: uniform stride
+  uint64_t stride;
+};
+inline ExpertLoc expert_loc(const mr_pack* p) {
+  if (p->uniform) return ExpertLoc{p->base + p->uni_off0, nullptr, p->uni_stride};
+  return ExpertLoc{p->base, p->d_offsets, 0};
+}
+}  // namespace mr
 
 struct mr_layer {
   mr_ctx* ctx = nullptr;

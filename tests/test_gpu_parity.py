@@ -327,6 +327,50 @@ def test_fused_repeated_launches_are_identical(gpu_ctx, layers, name):
         b.free()
 
 
+def _scattered_pack(ctx, ggml_type, data, n_exp, out_f, in_f):
+    """The same expert matrices stored in reverse order with a 256-byte gap after each:
+    offsets that are not one stride apart, so the kernels go through the offset table."""
+    mb = data.nbytes // n_exp
+    step = mb + 256
+    buf = np.zeros(n_exp * step, np.uint8)
+    offs = [(n_exp - 1 - e) * step for e in range(n_exp)]
+    for e, o in enumerate(offs):
+        buf[o:o + mb] = data[e * mb:(e + 1) * mb]
+    return M.ExpertPack.upload(ctx, ggml_type, buf, n_exp, out_f, in_f, offsets=offs)
+
+
+@pytest.mark.parametrize("name", ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-shared"])
+def test_fused_scattered_expert_offsets(gpu_ctx, layers, name):
+    """Packs with per-expert offsets (mr_pack_upload's host_offsets) give the same bits as
+    the contiguous packs the other tests use (those take the uniform-stride addressing)."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    H, I, E, t = spec.hidden, spec.inter, spec.n_experts, spec.ggml_type
+    packs = [_scattered_pack(gpu_ctx, t, host["gate"], E, I, H), _scattered_pack(gpu_ctx, t, host["up"], E, I, H),
+             _scattered_pack(gpu_ctx, t, host["down"], E, H, I)]
+    L = M.MoeLayer(gpu_ctx, *packs, router_w=dl.f["router_w"], router_b=dl.f["router_b"],
+                   gate_bias=dl.f["gate_b"], up_bias=dl.f["up_b"], down_bias=dl.f["down_b"],
+                   top_k=spec.top_k, route_flags=spec.route_flags, act=spec.act, alpha=spec.alpha,
+                   limit=spec.limit, sh_gate=dl.sh_gate, sh_up=dl.sh_up, sh_down=dl.sh_down,
+                   sh_gate_inp=dl.f["sh_gate_inp"])
+    x = W.x_tokens(spec, 3, first_token=70)
+    dx, y1, y2 = gpu_ctx.to_device(x), gpu_ctx.alloc(H * 4), gpu_ctx.alloc(H * 4)
+    try:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_FUSED)
+        for i in range(3):
+            xp = dx.ptr + i * H * 4
+            dl.layer.forward(xp, y1)
+            L.forward(xp, y2)
+            assert np.array_equal(y1.download(np.float32), y2.download(np.float32)), i
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+        L.close()
+        for p in packs:
+            p.close()
+        for b in (dx, y1, y2):
+            b.free()
+
+
 @pytest.mark.parametrize("name", ["tiny-mxfp4", "tiny-q4k-shared"])
 def test_fused_graph_replay(gpu_ctx, layers, name):
     dl, _ = get_layer(gpu_ctx, layers, name)
