@@ -284,6 +284,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   __shared__ int sel_i[16];
   __shared__ float sel_w[16];
   __shared__ int sel_o[16];
+  __shared__ uint32_t sel_k[16];
+  __shared__ uint32_t route_tmp[128];  // routing: compacted candidates
   __shared__ int ok_flag;
   __shared__ __align__(16) uint8_t lds_zero[32];
 
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     TRACE(1);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once its stream is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     XTRACE(wave);  // per wave: at the routing barrier
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     const int half = tail >= 0 ? 2 : (q < a.NS ? 1 : 0);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();

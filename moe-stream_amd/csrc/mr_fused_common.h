@@ -301,30 +301,110 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 
 constexpr int kRouteVals = 8;  // experts per lane in routing: E <= 512
 
-// (key desc, expert asc) compare-exchange of list entries a < b
-__device__ __forceinline__ void cas_desc(uint32_t& ka, int& ia, uint32_t& kb, int& ib) {
-  const bool sw = kb > ka || (kb == ka && ib < ia);
-  const uint32_t tk = sw ? kb : ka;
-  const int ti = sw ? ib : ia;
-  kb = sw ? ka : kb, ib = sw ? ia : ib;
-  ka = tk, ia = ti;
+// Lanes below this one in a 64-bit wave mask.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// The k-th largest key of the wave's NJ key columns: the largest T with at least k
+// keys >= T, fixed one bit at a time from the top (per bit, one ballot per column; the
+// compares issue before the first scalar count reads a mask). A lone wave issues about
+// one instruction per four cycles, so fewer instructions per bit beat fewer steps.
+template <int NJ>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[kRouteVals], int k) {
+  uint32_t T = 0u;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t t = T | (1u << b);
+    uint64_t m[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) m[j] = __ballot(key[j] >= t);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) c += __popcll(m[j]);
+    __builtin_amdgcn_sched_group_barrier(0x2, NJ, 0);
+    __builtin_amdgcn_sched_group_barrier(0x4, 2 * NJ + 3, 0);
+    T = c >= k ? t : T;
+  }
+  return T;
+}
+
+// The selected set: keys above T, then of the keys equal to T the lowest expert indices.
+// Expert indices idx[j] ascend with j, then with the lane (e = lane + 64*j, or a list
+// compacted in that order). Slot = rank of the expert index among the selected, so slots
+// run in ascending expert order. sel_i/sel_k[slot] get the expert and its key.
+template <int NJ>
+__device__ __forceinline__ void topk_slots(const uint32_t (&key)[kRouteVals], const int (&idx)[kRouteVals], int k,
+                                           int* sel_i, uint32_t* sel_k) {
+  const uint32_t T = kth_key<NJ>(key, k);
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) above += __popcll(__ballot(key[j] > T));
+  const int need = k - above;  // ties at T to take (>= 1)
+  int ties = 0, before = 0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint64_t eq = __ballot(key[j] == T);
+    const bool s = key[j] > T || (key[j] == T && ties + lanes_below(eq) < need);
+    ties += __popcll(eq);
+    const uint64_t sm = __ballot(s);
+    if (s) {
+      const int slot = before + lanes_below(sm);
+      sel_i[slot] = idx[j], sel_k[slot] = key[j];
+    }
+    before += __popcll(sm);
+  }
+}
+
+// Many columns (E > 128): the k-th largest lane maximum H bounds the threshold from
+// below (k lanes hold a key >= H), so only keys >= H can be selected. When those fit one
+// column they are compacted in ascending expert order through LDS (tmp: 128 words) and
+// selected there; otherwise all columns are searched.
+__device__ __forceinline__ void topk_slots_wide(const uint32_t (&key)[kRouteVals], int k, int* sel_i, uint32_t* sel_k,
+                                                uint32_t* tmp) {
+  const int lane = threadIdx.x & 63;
+  uint32_t hm[kRouteVals], hk = 0u;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) hk = max(hk, key[j]);
+  hm[0] = hk;
+  const uint32_t H = kth_key<1>(hm, k);
+  int before = 0;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    const bool s = key[j] >= H;
+    const uint64_t sm = __ballot(s);
+    const int slot = before + lanes_below(sm);
+    if (s && slot < 64) tmp[slot] = key[j], tmp[64 + slot] = (uint32_t)(lane + 64 * j);
+    before += __popcll(sm);
+  }
+  int idx[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
+  if (before > 64) {
+    topk_slots<kRouteVals>(key, idx, k, sel_i, sel_k);
+    return;
+  }
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+  uint32_t ck[kRouteVals];
+  ck[0] = lane < before ? tmp[lane] : 0u;
+  idx[0] = lane < before ? (int)tmp[64 + lane] : 0;
+  topk_slots<1>(ck, idx, k, sel_i, sel_k);
 }
 
 // Wave 0 of a consumer workgroup (all 64 lanes): wait until every logit of this
 // launch is published, then select the top-k (largest first, ties to the lower
 // index; top_k_routing layer.rs:2346-2403). Expert e = lane + 64*j is value j of
-// a lane; each lane sorts its values (Batcher network), then k rounds take the
-// wave-wide largest head (DPP max; ties: the lowest expert index) and pop it.
-// Writes slot -> (expert, weight) and ord[p] = the slot holding the p-th
-// smallest expert index (the combine order of layer.rs:1092-1106).
-// Selection part: poll the logits and pick the k experts; slot r's expert goes to sel_i[r]
-// (LDS) and, for route_finish, stays in the state (lane r = slot r).
+// a lane. Slots are numbered in ascending expert index, the combine order of
+// layer.rs:1092-1106; slot r's expert goes to sel_i[r] (LDS) and, for route_finish,
+// stays in the state (lane r = slot r).
 struct RouteState {
   float v[kRouteVals];  // this lane's logits
   uint32_t my_key;
   int my_e;
 };
-__device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, RouteState& st) {
+__device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, uint32_t* sel_k, uint32_t* tmp,
+                                   RouteState& st) {
   const int lane = threadIdx.x & 63;
   RTRACE(0);
   const int nj = (rc.E + 63) >> 6;  // values per lane (wave-uniform)
@@ -355,51 +435,27 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen
   // mode; exp is monotonic, so the order differs only where two logits round to the
   // same probability (a tie by value, which the tests treat as ambiguous).
-  // Weights: GPT-OSS (softmax over the k) and renormalised Qwen routing are the same
-  // softmax over the k selected logits; plain Qwen routing needs the all-expert sum.
-  RTRACE(3);
   uint32_t key[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j)  // + 0.f: -0.0 and +0.0 compare equal, so share a key
+    key[j] = (lane + 64 * j < rc.E) ? order_key(v[j] + 0.f) : 0u;
+  RTRACE(3);
   int idx[kRouteVals];
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j) {  // + 0.f: -0.0 and +0.0 compare equal, so share a key
-    key[j] = (lane + 64 * j < rc.E) ? order_key(v[j] + 0.f) : 0u;
-    idx[j] = lane + 64 * j;
-  }
-  if (nj == 2) {
-    cas_desc(key[0], idx[0], key[1], idx[1]);
-  } else if (nj > 2) {  // Batcher odd-even merge sort of 8
-#define MR_CAS(a, b) cas_desc(key[a], idx[a], key[b], idx[b])
-    MR_CAS(0, 1), MR_CAS(2, 3), MR_CAS(4, 5), MR_CAS(6, 7);
-    MR_CAS(0, 2), MR_CAS(1, 3), MR_CAS(4, 6), MR_CAS(5, 7);
-    MR_CAS(1, 2), MR_CAS(5, 6);
-    MR_CAS(0, 4), MR_CAS(1, 5), MR_CAS(2, 6), MR_CAS(3, 7);
-    MR_CAS(2, 4), MR_CAS(3, 5);
-    MR_CAS(1, 2), MR_CAS(3, 4), MR_CAS(5, 6);
-#undef MR_CAS
-  }
-  RTRACE(4);
-  uint32_t my_key = 0u;
-  int my_e = 0;
-  for (int r = 0; r < rc.k; ++r) {
-    const uint32_t M = wave_max_u(key[0]);
-    const unsigned long long tied = __ballot(key[0] == M);
-    int wl = __ffsll((long long)tied) - 1;
-    if (__popcll(tied) > 1)  // equal values: the lowest expert index wins
-      wl = (int)(wave_min_u(key[0] == M ? (uint32_t)idx[0] : 0xFFFFFFFFu) & 63u);
-    const int e = min(__builtin_amdgcn_readlane(idx[0], wl), rc.E - 1);
-    if (lane == r) my_key = M, my_e = e;
-    if (lane == wl) {  // pop the head
-#pragma unroll
-      for (int j = 0; j < kRouteVals - 1; ++j) key[j] = key[j + 1], idx[j] = idx[j + 1];
-      key[kRouteVals - 1] = 0u;
-    }
-  }
+  for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
+  if (nj <= 1)
+    topk_slots<1>(key, idx, rc.k, sel_i, sel_k);
+  else if (nj <= 2)
+    topk_slots<2>(key, idx, rc.k, sel_i, sel_k);
+  else
+    topk_slots_wide(key, rc.k, sel_i, sel_k, tmp);
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
   RTRACE(5);
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) st.v[j] = v[j];
-  st.my_key = my_key, st.my_e = my_e;
-  if (lane < rc.k) sel_i[lane] = my_e;
-  lds_drain();
+  st.my_key = lane < rc.k ? sel_k[lane] : 0u;
+  st.my_e = lane < rc.k ? sel_i[lane] : 0;
   RTRACE(7);
   return true;
 }
@@ -407,8 +463,9 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
 
 // Weights and combine order of the selection (the top-k weights of top_k_routing,
 // layer.rs:2346-2403; ascending expert order, layer.rs:1092-1106): sel_w[r] for slot r, and
-// ord[p] = the slot holding the p-th smallest expert index. Not needed to start streaming
-// weights, so callers run it after their first loads are issued.
+// ord[p] = the slot holding the p-th smallest expert index (slot p: slots ascend with the
+// expert index). Not needed to start streaming weights, so callers run it after their
+// first loads are issued.
 __device__ inline void route_finish(const RouteCfg& rc, const RouteState& st, float* sel_w, int* ord) {
   const int lane = threadIdx.x & 63;
   const float* v = st.v;
@@ -429,26 +486,14 @@ __device__ inline void route_finish(const RouteCfg& rc, const RouteState& st, fl
   const float l = in ? key_value(st.my_key) : 0.f;
   float w;
   if (sel_softmax) {
-    const float m = lane_f<0>(l);  // slot 0 holds the largest logit
+    const float m = wave_max_f(in ? l : -INFINITY);  // the largest selected logit
     const float ex = in ? __expf(l - m) : 0.f;
     w = ex / wave_sum_f(ex);
   } else {
     w = __expf(l - m_all) / s_all;
   }
-  int p = 0;  // position of this slot's expert in ascending expert order
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    if (r < rc.k) p += __builtin_amdgcn_readlane(st.my_e, r) < st.my_e ? 1 : 0;
-  if (in) sel_w[lane] = w, ord[p] = lane;
+  if (in) sel_w[lane] = w, ord[lane] = lane;
   lds_drain();
-}
-
-// Both parts in one call.
-__device__ inline bool route_wave(const RouteCfg& rc, uint32_t seq, int* sel_i, float* sel_w, int* ord) {
-  RouteState st;
-  if (!route_select(rc, seq, sel_i, st)) return false;
-  route_finish(rc, st, sel_w, ord);
-  return true;
 }
 
 __device__ __forceinline__ void fail(uint32_t* err) { st_sc1(err, 1u); }

@@ -243,6 +243,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   __shared__ int sel_i[16];
   __shared__ float sel_w[17];  // [k]: weight of the shared expert
   __shared__ int sel_o[16];
+  __shared__ uint32_t sel_k[16];
+  __shared__ uint32_t route_tmp[128];  // routing: compacted candidates
   __shared__ int ok_flag;
   __shared__ float gu_part[2][16];
   __shared__ __align__(16) int8_t hb[32];
@@ -344,7 +346,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     TRACE(1);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once its loads are issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();  // selection and the x image ready
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, rs)) {
+    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();

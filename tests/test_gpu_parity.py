@@ -498,3 +498,50 @@ def test_forward_residual_matches_oracle(gpu_ctx, layers, name):
         gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
     for b in (dn, dh, dout):
         b.free()
+
+
+# ---- fused routing: ties and many experts ----------------------------------------------
+
+TIE_SPECS = {
+    "mxfp4-E256": W.LayerSpec(210, 0, W.GGML_MXFP4, 256, 128, 256, 4, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                              W.ACT_SWIGLU_OAI, True, True),
+    "q4k-E300": W.LayerSpec(211, 0, W.GGML_Q4_K, 256, 256, 300, 10, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, True),
+    "q4k-E100": W.LayerSpec(212, 0, W.GGML_Q4_K, 256, 256, 100, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, True),
+}
+
+
+@pytest.mark.parametrize("pattern", ["all-equal", "tied-top", "distinct"])
+@pytest.mark.parametrize("name", list(TIE_SPECS))
+def test_fused_routing_ties_take_lowest_index(gpu_ctx, name, pattern):
+    """Router logits set through a zero router matrix and the router bias: all equal (every
+    expert ties), a tied top group (every 7th expert at the maximum, the rest distinct and
+    lower) and all distinct. The fused kernels must pick the oracle's experts (the largest,
+    ties to the lower index; layer.rs:2346-2403) and match its output."""
+    spec = TIE_SPECS[name]
+    E, k = spec.n_experts, spec.top_k
+    host = dict(spec=spec)
+    host.update(W.quant_tensors(spec))
+    host.update(W.float_tensors(spec))
+    host["router_w"] = np.zeros_like(host["router_w"])
+    b = np.zeros(E, np.float32)
+    if pattern != "all-equal":
+        b = (-1.0 - np.arange(E, dtype=np.float32) / E).astype(np.float32)[np.random.default_rng(9).permutation(E)]
+    if pattern == "tied-top":
+        b[::7] = 2.0
+    host["router_b"] = b
+    want = np.argsort(-b.astype(np.float64), kind="stable")[:k]
+    dl = W.DeviceLayer(gpu_ctx, spec, host=host)
+    L = oracle.layer_from_host(host)
+    x = W.x_tokens(spec, 2, first_token=80)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(spec.hidden * 4)
+    try:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_FUSED)
+        for t in range(2):
+            dl.layer.forward(dx.ptr + t * spec.hidden * 4, dy)
+            ry, ridx, _, _ = L.forward(x[t])
+            assert sorted(ridx[0].tolist()) == sorted(want.tolist())
+            assert rel_err(dy.download(np.float32), ry[0]) <= REL_TOL, (t, rel_err(dy.download(np.float32), ry[0]))
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+        dl.close()
+        dx.free(), dy.free()
