@@ -462,7 +462,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     const int half = tail >= 0 ? 2 : (q < a.NS ? 1 : 0);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
+    if (wave == 0 && !route_select<MR_ROUTE_SLEEP_DOWN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
       if (slot < a.k) prep_rows(rd, sh, nbI, g);  // waits for the weights: they land long before gate/up ends
       TRACE(2);
-      if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);

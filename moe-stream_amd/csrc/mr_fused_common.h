@@ -24,7 +24,11 @@ constexpr int kCopies = 64;     // copies of each producer counter, one 128-byte
 constexpr int kCopyStride = 32;  // words
 constexpr int kMaxLogits = 1024;
 constexpr int kMaxGrid = 1024;
-constexpr int kLogitCopies = 32;  // copies of the published logits (consumers spread their polls)
+#ifndef MR_LOGIT_COPIES
+#define MR_LOGIT_COPIES 32
+#endif
+constexpr int kLogitCopies = MR_LOGIT_COPIES;  // copies of the published logits (consumers spread their polls)
+static_assert(kLogitCopies >= 1 && kLogitCopies <= 64, "one copy per lane of the publishing wave");
 enum : int {
   FS_GU = 0,                                   // [kCopies] counter: gate/up units finished
   FS_WGSEQ = FS_GU + kCopies * kCopyStride,    // [grid] launches completed, one word per workgroup
@@ -195,6 +199,9 @@ __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u)
 // Bounded wait (one full wave) until the counter copies sum to at least `target`
 // (wrap-around safe); false if the limit ran out. SLEEP: s_sleep units (64 clocks)
 // between polls (longer for waits that overlap weight streaming).
+#ifndef MR_GU_WAIT_SLEEP
+#define MR_GU_WAIT_SLEEP 32  // the down workgroups' wait for the gate/up count
+#endif
 template <int SLEEP = 2>
 __device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
   const int lane = threadIdx.x & 63;
@@ -300,6 +307,14 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 }
 
 constexpr int kRouteVals = 8;  // experts per lane in routing: E <= 512
+// s_sleep units (64 clocks) between polls of the published logits: every workgroup polls,
+// so the poll rate is weighed against the traffic it adds to the lines being waited on.
+#ifndef MR_ROUTE_SLEEP
+#define MR_ROUTE_SLEEP 2
+#endif
+#ifndef MR_ROUTE_SLEEP_DOWN
+#define MR_ROUTE_SLEEP_DOWN 100  // down workgroups: their weights are needed only after gate/up
+#endif
 
 // Lanes below this one in a 64-bit wave mask.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
@@ -403,6 +418,7 @@ struct RouteState {
   uint32_t my_key;
   int my_e;
 };
+template <int SLEEP = MR_ROUTE_SLEEP>
 __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, uint32_t* sel_k, uint32_t* tmp,
                                    RouteState& st) {
   const int lane = threadIdx.x & 63;
@@ -429,7 +445,7 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
     if (ex >= 0) ok = ok && (uint32_t)(ld64_sc1(lw + ex) >> 32) == flag;
     if (__ballot(!ok) == 0ull) break;
     if (it >= rc.spin_limit) return false;
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(SLEEP);
   }
   RTRACE(1);
   // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen

@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     const int q = bid - a.R;
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
+    if (wave == 0 && !route_select<MR_ROUTE_SLEEP_DOWN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     __syncthreads();
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       float* vbuf = reinterpret_cast<float*>(smem + kDnVbuf) + wave * kDnSbW * 9;
       region_headers<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, reinterpret_cast<uint4*>(vbuf), hdec);
       TRACE(2);
-      if (wave == 0 && !wait_count<8>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);
