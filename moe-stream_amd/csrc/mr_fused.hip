@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       TRACE(4);
     }
     // counted even when routing failed, so later launches stay in step
-    if (tid == 0) count(a.fs + FS_GU, gid);
+    if (tid == 0) count<64>(a.fs + FS_GU, gid);
   } else {
     // ------------------------------------------------------------- down
     // Row group q of 16 output rows. The first NS groups are split: rows 0-7 here, rows
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
       if (slot < a.k) prep_rows(rd, sh, nbI, g);  // waits for the weights: they land long before gate/up ends
       TRACE(2);
-      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 64>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);

@@ -20,7 +20,7 @@
 
 namespace mr {
 
-constexpr int kCopies = 64;     // copies of each producer counter, one 128-byte line apart
+constexpr int kCopies = 128;    // room for this many copies of each producer counter, one 128-byte line apart
 constexpr int kCopyStride = 32;  // words
 constexpr int kMaxLogits = 1024;
 constexpr int kMaxGrid = 1024;
@@ -191,9 +191,12 @@ __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" :
 // All LDS operations this wave has issued have completed.
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Count n finished producer items on copy (id % kCopies) (no return value is waited for).
+// Count n finished producer items on copy (id % NC) (no return value is waited for).
+// NC copies in use (64 or 128: fewer lines to poll against fewer producers per line).
+template <int NC>
 __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u) {
-  (void)__hip_atomic_fetch_add(copies + kCopyStride * (id % kCopies), n, __ATOMIC_RELAXED,
+  static_assert(NC == 64 || NC == 128, "one or two copies per lane of the waiting wave");
+  (void)__hip_atomic_fetch_add(copies + kCopyStride * (id % NC), n, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
 }
 // Bounded wait (one full wave) until the counter copies sum to at least `target`
@@ -202,11 +205,13 @@ __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u)
 #ifndef MR_GU_WAIT_SLEEP
 #define MR_GU_WAIT_SLEEP 32  // the down workgroups' wait for the gate/up count
 #endif
-template <int SLEEP = 2>
+template <int SLEEP, int NC>
 __device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
   const int lane = threadIdx.x & 63;
   for (uint32_t it = 0;; ++it) {
-    const uint32_t sum = wave_sum_u(ld_sc1(copies + kCopyStride * lane));
+    uint32_t c = ld_sc1(copies + kCopyStride * lane);
+    if (NC > 64) c += ld_sc1(copies + kCopyStride * (lane + 64));
+    const uint32_t sum = wave_sum_u(c);
     if ((int32_t)(sum - target) >= 0) return true;
     if (it >= limit) return false;
     __builtin_amdgcn_s_sleep(SLEEP);
