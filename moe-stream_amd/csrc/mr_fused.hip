@@ -300,6 +300,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
+    __builtin_amdgcn_s_setprio(2);  // the logits gate every other role: router loads issue first
     const int e = bid * 4 + wave;
     if (e < a.E) {
       const float* w = a.router_w + (size_t)e * a.H;
@@ -341,6 +342,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   } else if (bid >= a.R + a.ND && bid < a.R + a.ND + a.NG) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
+    // The gate/up streams issue ahead of the down workgroups' weight prefetch on the same
+    // CU (those weights are needed only once every gate/up unit is done).
+    __builtin_amdgcn_s_setprio(1);
     const int nrp = a.I >> 5;
     // x split image in LDS (independent of routing): 8 lanes per block, all
     // loads issued first

@@ -259,6 +259,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
+    __builtin_amdgcn_s_setprio(2);  // the logits gate every other role: router loads issue first
     const int e = bid * 4 + wave;
     if (e < a.E + a.has_sh) {
       const float* w = e < a.E ? a.router_w + (size_t)e * a.H : a.sh_gate_inp;
@@ -302,6 +303,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   } else if (bid >= a.R + a.ND) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
+    // the gate/up loads issue ahead of the down workgroups' prefetch on the same CU
+    __builtin_amdgcn_s_setprio(1);
     uint8_t* xq = smem + kGuXq;
     float2* xs = reinterpret_cast<float2*>(smem + kGuXs);
     // x = rms_norm(h) when fused: each wave derives inv the way the router waves do
