@@ -205,18 +205,25 @@ __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u)
 #ifndef MR_GU_WAIT_SLEEP
 #define MR_GU_WAIT_SLEEP 32  // the down workgroups' wait for the gate/up count
 #endif
-template <int SLEEP, int NC>
-__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit) {
+// Once at most `near` items are missing, polls come every SLEEP_NEAR units instead: the
+// last producers are seen sooner without polling fast through the whole wait.
+template <int SLEEP, int NC, int SLEEP_NEAR = SLEEP>
+__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit, uint32_t near = 0u) {
   const int lane = threadIdx.x & 63;
   for (uint32_t it = 0;; ++it) {
     uint32_t c = ld_sc1(copies + kCopyStride * lane);
     if (NC > 64) c += ld_sc1(copies + kCopyStride * (lane + 64));
     const uint32_t sum = wave_sum_u(c);
-    if ((int32_t)(sum - target) >= 0) return true;
+    const int32_t missing = (int32_t)(target - sum);
+    if (missing <= 0) return true;
     if (it >= limit) return false;
-    __builtin_amdgcn_s_sleep(SLEEP);
+    if ((uint32_t)missing <= near)
+      __builtin_amdgcn_s_sleep(SLEEP_NEAR);
+    else
+      __builtin_amdgcn_s_sleep(SLEEP);
   }
 }
+
 
 // ---- fused RMSNorm and residual (norm.rs:16-37; layer.rs:462-473) ---------------------------
 // mr_moe_forward_residual: the layer's input is rms_norm(h) = (h * inv) * w with

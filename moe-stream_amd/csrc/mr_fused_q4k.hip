@@ -446,7 +446,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       float* vbuf = reinterpret_cast<float*>(smem + kDnVbuf) + wave * kDnSbW * 9;
       region_headers<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, reinterpret_cast<uint4*>(vbuf), hdec);
       TRACE(2);
-      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit,
+                                                         (uint32_t)a.NG / 4) && lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);
