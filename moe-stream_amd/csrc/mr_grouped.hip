@@ -97,10 +97,8 @@ __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ sr
 
 // ---- grouped GEMM -------------------------------------------------------------------------
 struct GroupedArgs {
-  const uint8_t* w0;  // gate (GATEUP) or down
-  const uint8_t* w1;  // up (GATEUP)
-  const uint64_t* off0;
-  const uint64_t* off1;
+  ExpertLoc w0;  // gate (GATEUP) or down
+  ExpertLoc w1;  // up (GATEUP)
   const float* b0;  // gate bias [E][M] (GATEUP) or null
   const float* b1;  // up bias
   const uint8_t* img;    // B images [rows][K/32][kImgBytes]
@@ -110,41 +108,60 @@ struct GroupedArgs {
   const int32_t* exp_off;
   const int32_t* tile_off;
   float* out;  // [P][M]
-  int M, K, E, max_tiles;
+  int M, K, E;
   int act;
   float alpha, limit;
 };
 
-// Grouped GEMM work item: (expert e, row tile, 32-pair tile). 8 waves; each wave owns
-// 16 output rows of one matrix (gate/up: waves 0-3 gate, 4-7 up, the same 64 rows;
-// down: 8 x 16 = 128 rows) and all 32 pairs (8 MFMA column groups of 4 pairs x 4 terms).
-// K advances one MFMA step (4 blocks) at a time through double-buffered LDS:
-//   B: the step's 32 pairs x 4 blocks x 128-byte images (16 KB), loaded cooperatively
-//      by direct global->LDS loads (each pair's 512 bytes are contiguous) and shared
-//      by the 8 waves;
-//   A: each wave's 16 rows x 68 bytes, fetched as 6 aligned 16-byte pieces per row by
-//      direct global->LDS loads (rows are 1530 bytes apart, so a wave load covers ~10
-//      rows' contiguous bytes instead of 16 scattered block windows).
-constexpr int kGemmWaves = 8;
-constexpr int kAPieces = 6;                         // pieces per row and step: 15 + 68 + 3 <= 96
-constexpr int kAStage = 2 * 1024;                   // one A buffer: 96 pieces + pad (2 wave loads)
-constexpr int kBStage = kPairTile * 4 * kImgBytes;  // one B buffer: 32 pairs x 4 blocks
-static_assert(kPairTile * 4 * 8 == 2 * 512, "two B pieces per thread per step");
+// Grouped GEMM work item: (expert e, row tile, 32-pair tile); 4 waves. A wave owns kGT
+// 16-row A tiles of one matrix (gate/up: waves 0-1 gate, 2-3 up, the same 96 rows; down:
+// 4 x 48 = 192 rows) and the tile's 32 pairs as 2 groups of 16.
+// One MFMA covers 16 rows x 1 weight block x 16 pairs, with the 4 e4m3 terms of the pairs'
+// activation block along K: K group j of the MFMA is term j, so the A operand is the
+// weight block repeated in every K group (each with the block's scale byte) and B's
+// group j is term j of the 16 pairs (with term j's scale byte). D then holds the term-summed
+// dot product of row x pair: no term columns to add afterwards, 16 pairs per MFMA, and a
+// wave keeps kGT x 2 accumulator tiles.
+// K advances 4 blocks per step:
+//   A: each row's 68 bytes of a step as 6 aligned 16-byte pieces, lane-contiguous (a wave
+//      load covers ~11 rows' contiguous bytes; 20-byte windows loaded per lane straight
+//      from global cost 3x the L1 accesses), two steps ahead in registers, then written to
+//      the wave's LDS slice, from which the 4 lanes of a row read the same block window;
+//   B: the step's 32 pairs x 4 blocks x 128-byte images (16 KB) and their scale words, two
+//      steps ahead in registers (4 pieces per thread), then written to a double-buffered LDS
+//      stage shared by the 4 waves. (Direct global->LDS loads would save the registers, but
+//      the compiler then waits for all of them before any LDS read, which serialises the
+//      prefetch.) 16-byte part q of (pair pr, block b) sits in slot b_slot(pr, b, q),
+//      so the 16 lanes of a read (16 pairs, one part) hit 16 different bank groups.
+constexpr int kGW = 4;               // waves per work item
+constexpr int kGT = 3;               // 16-row A tiles per wave
+constexpr int kPG = kPairTile / 16;  // 16-pair MFMA column groups
+constexpr int kBStep = kPairTile * 4 * kImgBytes;  // B bytes per K step
+constexpr int kAPR = 6;                            // A pieces per row and step: 68 bytes at any offset
+constexpr int kASlots = kGT * 16 * kAPR;           // A pieces per wave and step
+constexpr int kAK = (kASlots + 63) / 64;           // A piece loads per lane and step
+constexpr int kARow = 104;  // LDS bytes per A row: 26 dwords, so 16 rows fall in 16 different banks
+constexpr int kBBuf = 2;                           // B stages in LDS
+static_assert(kBStep == 4 * kGW * 64 * 16, "four 16-byte pieces per thread per step");
+static_assert(kPairTile * 4 == 2 * 64, "scale words: one per lane of waves 0-1");
+static_assert(kTerms == 4, "one term per MFMA K group");
+
+// LDS slot of 16-byte part q of (pair pr, block b) in a B stage: the 16 pairs that one read
+// instruction's lanes take (one part each) land in 16 different 16-byte bank groups.
+__device__ __forceinline__ int b_slot(int pr, int b, int q) { return pr * 32 + (b ^ ((pr >> 3) & 1)) * 8 + (q ^ (pr & 7)); }
 
 template <bool GATEUP>
-__global__ __launch_bounds__(512, 2) void k_grouped_gemm(GroupedArgs a) {
-  __shared__ __align__(16) uint8_t bst[2][kBStage];
-  __shared__ __align__(16) uint32_t bsc[2][kPairTile * 4];
-  __shared__ __align__(16) uint8_t ast[kGemmWaves][2][kAStage];
-  __shared__ __align__(16) uint8_t zero[32];
+__global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
+  __shared__ __align__(16) uint8_t bst[kBBuf][kBStep];
+  __shared__ __align__(16) uint32_t bsc[kBBuf][kPairTile * 4];
+  __shared__ __align__(16) uint8_t ast[kGW][kGT * 16 * kARow];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int i = lane & 15, g = lane >> 4, t = i & 3;
-  constexpr int NM = GATEUP ? 2 : 1;
-  constexpr int kRows = 16 * kGemmWaves / NM;  // rows per work item
-  // Work items are ordered (expert, row tile, pair tile of the expert), and each
-  // XCD (workgroups are dispatched round-robin over kXcds) takes one contiguous
-  // range of them: the items that share an expert's row tile (A) or its pairs'
-  // images (B) run on the same XCD and meet in its L2.
+  const int i = lane & 15, g = lane >> 4;
+  constexpr int kRows = GATEUP ? (kGW / 2) * kGT * 16 : kGW * kGT * 16;  // rows of a matrix per item
+  // Work items are ordered (expert, row tile, pair tile of the expert), and each XCD
+  // (workgroups are dispatched round-robin over kXcds) takes one contiguous range of them:
+  // the items that share an expert's row tile (A) or its pairs' images (B) run on the same
+  // XCD and meet in its L2.
   const int n_rt = (a.M + kRows - 1) / kRows;
   const int n_work = n_rt * a.tile_off[a.E];
   const int per_xcd = (n_work + kXcds - 1) / kXcds;
@@ -162,136 +179,189 @@ __global__ __launch_bounds__(512, 2) void k_grouped_gemm(GroupedArgs a) {
   const int rt = wl / nt_e, tl = wl - rt * nt_e;
   const int p0 = a.exp_off[e] + tl * kPairTile;
   const int np = min(kPairTile, a.exp_off[e + 1] - p0);
-  if (tid < 8) reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
+  const int npg = (np + 15) >> 4;  // pair groups holding pairs (uniform)
 
   const int nbK = a.K >> 5, S = (nbK + 3) >> 2;
   const uint64_t rb = (uint64_t)nbK * 17;
-  const int m = GATEUP ? (wave >> 2) : 0;
-  const int row0 = rt * kRows + (GATEUP ? (wave & 3) : wave) * 16;
-  const bool rows_in = row0 < a.M;          // wave-uniform; other waves still load B and sync
-  const int row0c = min(row0, a.M - 16);    // M is a multiple of 16
-  const uint8_t* W = (m ? a.w1 + a.off1[e] : a.w0 + a.off0[e]) + (uint64_t)row0c * rb;
-  // this thread's B pieces (q = j*512 + tid): pair q/32, block (q/8)%4, part q%8
-  const uint8_t* bsrc[2];
+  const int m = GATEUP ? (wave >> 1) : 0;
+  const int wrow0 = rt * kRows + (GATEUP ? (wave & 1) : wave) * (kGT * 16);
+  const uint8_t* W = expert_at(m ? a.w1 : a.w0, e);
+  bool tin[kGT];  // tile inside the matrix (wave-uniform)
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int q = j * 512 + tid;
-    const int p = p0 + min(q >> 5, np - 1);
-    const int r = a.pair_tok ? a.pair_tok[p] : p;
-    bsrc[j] = a.img + (size_t)r * nbK * kImgBytes + (q & 7) * 16;
+  for (int tt = 0; tt < kGT; ++tt) tin[tt] = wrow0 + 16 * tt < a.M;
+  // This lane's row i: its rows in every tile are 16 rows (a multiple of 16 bytes) apart,
+  // so the byte position of a block in its 16-byte piece is the same for all of them.
+  const uintptr_t row_i = reinterpret_cast<uintptr_t>(W) + (uintptr_t)min(wrow0 + i, a.M - 1) * rb;
+  const uint32_t lead0 = (uint32_t)row_i & 15u;  // row start within its piece
+  // A piece slots of this lane: slot k*64 + lane = (tile, row, piece) of the wave's rows
+  const uint8_t* aps[kAK];
+  int apc[kAK], aslot[kAK];
+#pragma unroll
+  for (int k = 0; k < kAK; ++k) {
+    const int sl = min(k * 64 + lane, kASlots - 1);
+    const int tt = sl / (16 * kAPR), rr = (sl / kAPR) % 16;
+    apc[k] = sl % kAPR;
+    aps[k] = W + (uint64_t)min(wrow0 + 16 * tt + rr, a.M - 1) * rb;
+    aslot[k] = (tt * 16 + rr) * kARow + apc[k] * 16;
   }
-  const int sq = tid & 127;  // scale word sq (waves 0-1): pair sq/4, block sq%4
-  const uint32_t* ssrc;
+
+  // B pieces of this thread: slot j*256 + tid = (pair j*8 + bpl, block bb, stored part bq)
+  const int bq = tid & 7, bb = (tid >> 3) & 3, bpl = tid >> 5;
+  const uint8_t* bsrc[4];
+  int bslot[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bslot[j] = b_slot(j * 8 + bpl, bb, bq);
+    const int p = p0 + min(j * 8 + bpl, np - 1);
+    const int r = a.pair_tok ? a.pair_tok[p] : p;
+    bsrc[j] = a.img + (size_t)r * nbK * kImgBytes + bq * 16;
+  }
+  const uint32_t* ssrc;  // scale word tid (waves 0-1): pair tid/4, block tid%4
   {
-    const int p = p0 + min(sq >> 2, np - 1);
+    const int p = p0 + min((tid & 127) >> 2, np - 1);
     const int r = a.pair_tok ? a.pair_tok[p] : p;
     ssrc = a.isc + (size_t)r * nbK;
   }
-  // A pieces of this wave (p = it*64 + lane): row p/6, piece p%6 (p >= 96: pad)
-  const uint8_t* arow[2];
-  int apc[2];
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int pp = it * 64 + lane;
-    const int r = min(pp / kAPieces, 15);
-    apc[it] = min(pp - r * kAPieces, kAPieces - 1);
-    arow[it] = W + (uint64_t)r * rb;
-  }
-  const uintptr_t my_row = reinterpret_cast<uintptr_t>(W + (uint64_t)i * rb);
-
-  auto issue = [&](int st, int buf) {
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const uintptr_t first = reinterpret_cast<uintptr_t>(arow[it] + (size_t)(4 * st) * 17) & ~(uintptr_t)15;
-      const uintptr_t last = (reinterpret_cast<uintptr_t>(arow[it] + (size_t)nbK * 17) - 1) & ~(uintptr_t)15;
-      const uintptr_t src = min(first + 16 * (uintptr_t)apc[it], last);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), &ast[wave][buf][it * 1024], 16, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int q = j * 512 + tid;
-      const int blk = min(4 * st + ((q >> 3) & 3), nbK - 1);
-      __builtin_amdgcn_global_load_lds(bsrc[j] + (size_t)blk * kImgBytes, &bst[buf][(j * 512 + wave * 64) * 16], 16,
-                                       0, 0);
-    }
-    if (wave < 2)
-      __builtin_amdgcn_global_load_lds(ssrc + min(4 * st + (sq & 3), nbK - 1), &bsc[buf][wave * 64], 4, 0, 0);
+  struct BRegs {
+    i32x4 v[4];
+    uint32_t sc;
   };
-
-  f32x4 acc[8];
+  auto load_b = [&](int st, BRegs& br) {
+    const size_t boff = (size_t)min(4 * st + bb, nbK - 1) * kImgBytes;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  issue(0, 0);
-  for (int st = 0; st < S; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < S) {
-      __syncthreads();  // every wave is done with buffer buf^1 (step st-1)
-      issue(st + 1, buf ^ 1);
-      if (wave < 2)
-        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // step st's loads have landed
-      else
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
-      vm_drain();
+    for (int j = 0; j < 4; ++j) br.v[j] = *(const __attribute__((address_space(1))) i32x4*)(bsrc[j] + boff);
+    br.sc = *(const __attribute__((address_space(1))) uint32_t*)(ssrc + min(4 * st + (tid & 3), nbK - 1));
+  };
+  auto store_b = [&](const BRegs& br, int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<i32x4*>(&bst[buf][bslot[j] * 16]) = br.v[j];
+    if (wave < 2) bsc[buf][tid] = br.sc;
+  };
+  auto load_a = [&](int st, i32x4 (&apv)[kAK]) {  // pieces past the row end read its last piece
+#pragma unroll
+    for (int k = 0; k < kAK; ++k) {
+      const uintptr_t first = (reinterpret_cast<uintptr_t>(aps[k]) + (uintptr_t)(68 * st)) & ~(uintptr_t)15;
+      const uintptr_t last = (reinterpret_cast<uintptr_t>(aps[k]) + (uintptr_t)(17 * nbK) - 1) & ~(uintptr_t)15;
+      const uintptr_t src = min(first + 16 * (uintptr_t)apc[k], last);
+      apv[k] = *(const __attribute__((address_space(1))) i32x4*)src;
     }
-    __syncthreads();  // step st's A and B are in LDS for every wave
-    if (rows_in) {
-      const int b = 4 * st + g;  // this lane's A block
-      const int lead = (int)((my_row + (uintptr_t)(4 * st) * 17) & 15u);
-      const int off = i * (kAPieces * 16) + lead + g * 17;
-      const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][buf][off & ~3]);
-      RawBlk ra;
-      ra.d[0] = wp[0], ra.d[1] = wp[1], ra.d[2] = wp[2], ra.d[3] = wp[3], ra.d[4] = wp[4];
-      const int b0 = 4 * st + (g >> 1), b1 = b0 + 2;
-      const int sb_off = (b < nbK ? g : 0);
+  };
+  auto store_a = [&](const i32x4 (&apv)[kAK]) {  // slots past kASlots are not stored
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int pr = 4 * c + (i >> 2);
-        const uint8_t* pb = &bst[buf][pr * 4 * kImgBytes + t * 32 + 16 * (g & 1)];
-        const i32x4 v0 = *reinterpret_cast<const i32x4*>(b0 < nbK ? pb + (g >> 1) * kImgBytes : zero);
-        const i32x4 v1 = *reinterpret_cast<const i32x4*>(b1 < nbK ? pb + (2 + (g >> 1)) * kImgBytes : zero);
-        const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        const int sb = (int)((bsc[buf][pr * 4 + sb_off] >> (8 * t)) & 0xFFu);
-        acc[c] = mfma_raw(ra, (uint32_t)off & 3u, b < nbK, B, sb, acc[c]);
-      }
-    }
-  }
-  // epilogue: columns 4*tl .. 4*tl+3 of group c are the 4 terms of pair 4c+tl
-  float* xch = reinterpret_cast<float*>(&bst[0][0]);  // gate results for the up waves (32 KB)
-  if (GATEUP) {
-    __syncthreads();  // the K loop's LDS is no longer read
-    if (m == 0) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xch[(((wave & 3) * 8 + c) * 4 + r) * 64 + lane] = sum4(acc[c][r]);
-    }
-    __syncthreads();
-    if (m == 0) return;
-  }
-  if (!rows_in) return;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = sum4(acc[c][r]);
-      const int pl = 4 * c + (i >> 2);
-      const int orow = row0 + 4 * g + r;
-      if (t == 0 && pl < np && orow < a.M) {
-        const int p = p0 + pl;
-        float o;
-        if (GATEUP) {
-          float gv = xch[(((wave & 3) * 8 + c) * 4 + r) * 64 + lane], uv = v;
-          if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
-          if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
-          const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-          o = h * a.pair_w[p];
-        } else {
-          o = v;
+    for (int k = 0; k < kAK; ++k)
+      if (k * 64 + 64 <= kASlots || k * 64 + lane < kASlots)
+        {  // 8-byte aligned: rows are kARow bytes apart
+          uint64_t* d = reinterpret_cast<uint64_t*>(&ast[wave][aslot[k]]);
+          d[0] = ((uint64_t)(uint32_t)apv[k][1] << 32) | (uint32_t)apv[k][0];
+          d[1] = ((uint64_t)(uint32_t)apv[k][3] << 32) | (uint32_t)apv[k][2];
         }
-        a.out[(size_t)p * a.M + orow] = o;
+  };
+  // B reads of lane (pair n = i of the group, K group g): parts g (term g/2, half g%2) and
+  // g + 4 (term 2 + g/2) of (pair, block); pairs of the two groups differ by 16 (same swizzle)
+  int brd[4][2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) brd[k][h] = b_slot(i, k, g + 4 * h) * 16;
+  const int srd = i * 16 + g;  // scale byte of pair i, block 0, term g (block k: +4k; group: +256)
+
+  f32x4 acc[kGT][kPG];
+#pragma unroll
+  for (int tt = 0; tt < kGT; ++tt)
+#pragma unroll
+    for (int pg = 0; pg < kPG; ++pg) acc[tt][pg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Step st: pieces in register set st % 2, B in LDS buffer st % 2; the loads of step st + 2
+  // reuse the register set once it has been written to LDS.
+  // Every step issues the same loads (past the last step: the last step's data again), so
+  // the compiler's waits before the LDS writes count exactly one step's loads in flight.
+  auto step = [&](int st, i32x4 (&cur)[kAK], BRegs& bcur) {
+    const int buf = st % kBBuf;
+    store_a(cur);        // this wave's A slice (its reads of step st-1 are done: LDS ops stay in order)
+    store_b(bcur, buf);  // buffer st % 2 was last read in step st-2, before the previous barrier
+    __syncthreads();     // step st's B stage is complete
+    load_b(min(st + 2, S - 1), bcur);
+    load_a(min(st + 2, S - 1), cur);
+    const uint8_t* bb_base = &bst[buf][0];
+    const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
+    const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (4 * st + k < nbK) {  // uniform: blocks past the row end are skipped
+        // A: window of block 4 st + k of this lane's row in each tile (the 4 K groups of a
+        // row read the same window)
+        const uint32_t wo = lead + 17u * (uint32_t)k;
+        const uint32_t t8 = 8u * ((wo & 3u) + 1u);
+        AOp ao[kGT];
+        int sa[kGT];
+#pragma unroll
+        for (int tt = 0; tt < kGT; ++tt) {
+          const uint32_t* wp =
+              reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
+          RawBlk r;
+          r.d[0] = wp[0], r.d[1] = wp[1], r.d[2] = wp[2], r.d[3] = wp[3], r.d[4] = wp[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ao[tt].q[q] = (uint32_t)((((uint64_t)r.d[q + 1] << 32) | r.d[q]) >> t8);
+          sa[tt] = (int)((r.d[0] >> (8u * (wo & 3u))) & 0xFFu);
+        }
+#pragma unroll
+        for (int pg = 0; pg < kPG; ++pg) {
+          if (pg < npg) {
+            const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
+            const i32x4 v0 = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
+            const i32x4 v1 = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
+            const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            const int sb = (int)sc_base[srd + pg * 256 + 4 * k];
+#pragma unroll
+            for (int tt = 0; tt < kGT; ++tt)
+              if (tin[tt]) acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
+          }
+        }
       }
     }
+  };
+  i32x4 apA[kAK], apB[kAK];
+  BRegs bA, bB;
+  load_b(0, bA);
+  load_a(0, apA);
+  load_b(min(1, S - 1), bB);
+  load_a(min(1, S - 1), apB);
+  int st = 0;
+  for (; st + 1 < S; st += 2) {
+    step(st, apA, bA);
+    step(st + 1, apB, bB);
+  }
+  if (st < S) step(st, apA, bA);
+
+  // Epilogue: acc[tt][pg][r] of lane (i, g) is row wrow0 + 16 tt + 4g + r x pair 16 pg + i.
+  // The wave's block goes through LDS as [pair][row] so that each pair's rows are stored
+  // contiguously (and the up waves find the gate values of their rows there).
+  __syncthreads();  // the K loop's LDS is no longer read
+  constexpr int kWR = kGT * 16;                                  // rows of a wave
+  float* blk = reinterpret_cast<float*>(&bst[0][0]) + wave * kPairTile * kWR;  // [pair][row]
+#pragma unroll
+  for (int tt = 0; tt < kGT; ++tt)
+#pragma unroll
+    for (int pg = 0; pg < kPG; ++pg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) blk[(pg * 16 + i) * kWR + tt * 16 + 4 * g + r] = acc[tt][pg][r];
+  __syncthreads();
+  if (GATEUP && m == 0) return;
+  const float* gblk = reinterpret_cast<const float*>(&bst[0][0]) + (wave & 1) * kPairTile * kWR;  // gate
+  for (int q = lane; q < np * kWR; q += 64) {
+    const int pl = q / kWR, rr = q - pl * kWR;
+    const int orow = wrow0 + rr;
+    if (orow >= a.M) continue;
+    const int p = p0 + pl;
+    float o = blk[pl * kWR + rr];
+    if (GATEUP) {
+      float gv = gblk[pl * kWR + rr], uv = o;
+      if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
+      if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
+      const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
+      o = h * a.pair_w[p];
+    }
+    a.out[(size_t)p * a.M + orow] = o;
   }
 }
 
@@ -394,15 +464,17 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   GroupedArgs a{};
-  a.w0 = L.d.gate->base, a.w1 = L.d.up->base, a.off0 = L.d.gate->d_offsets, a.off1 = L.d.up->d_offsets;
+  a.w0 = expert_loc(L.d.gate), a.w1 = expert_loc(L.d.up);
   a.b0 = L.d.gate_bias, a.b1 = L.d.up_bias;
   a.img = gs.img_x, a.isc = gs.sc_x, a.pair_tok = gs.pair_tok, a.pair_w = gs.pair_w;
   a.exp_off = gs.exp_off, a.tile_off = gs.tile_off, a.out = gs.hbuf;
-  a.M = I, a.K = H, a.E = E, a.max_tiles = max_tiles;
+  a.M = I, a.K = H, a.E = E;
   a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   {
     ProfScope ps(K, "grouped_gateup");
-    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + 63) / 64) * max_tiles)), dim3(512), 0, K.s, a);
+    constexpr int rows = (kGW / 2) * kGT * 16;
+    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
+                       K.s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
@@ -413,13 +485,15 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   GroupedArgs d{};
-  d.w0 = L.d.down->base, d.off0 = L.d.down->d_offsets;
+  d.w0 = expert_loc(L.d.down);
   d.img = gs.img_h, d.isc = gs.sc_h, d.pair_tok = nullptr, d.pair_w = gs.pair_w;
   d.exp_off = gs.exp_off, d.tile_off = gs.tile_off, d.out = gs.obuf;
-  d.M = H, d.K = I, d.E = E, d.max_tiles = max_tiles;
+  d.M = H, d.K = I, d.E = E;
   {
     ProfScope ps(K, "grouped_down");
-    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3((unsigned)(((H + 127) / 128) * max_tiles)), dim3(512), 0, K.s, d);
+    constexpr int rows = kGW * kGT * 16;
+    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3((unsigned)(((H + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
+                       K.s, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
