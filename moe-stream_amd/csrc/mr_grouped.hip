@@ -4,9 +4,8 @@
 // The reference runs each expert once over all of its tokens: index_select of
 // the expert's tokens, gate/up/act/down, x routing weight, index_add back
 // (layer.rs:2148-2183; CPU: mxfp4_matmul per expert, layer.rs:1449-1514). Here:
-//   k_group       (token, slot) pairs sorted by (expert, token, slot); per-expert
-//                 pair offsets and 32-pair tile offsets; pair index of every
-//                 (token, slot).
+//   k_group       (token, slot) pairs grouped by expert; per-expert pair offsets and
+//                 32-pair tile offsets; pair index of every (token, slot).
 //   k_split_rows  activation rows -> e4m3 B images (4 terms per 32-element block).
 //   k_grouped_gemm<true>   gate and up for one (expert, 64-row tile, 32-pair tile):
 //                 A = native MXFP4 weight rows, B = the 16 pairs' x images; epilogue
@@ -24,6 +23,7 @@
 #include "mr_mx_mfma.h"
 
 #include <algorithm>
+#include <climits>
 
 namespace mr {
 
@@ -32,44 +32,60 @@ constexpr int kXcds = 8;        // MI355X accelerator complex dies (one L2 each)
 constexpr int kMaxSteps = 32;   // K steps (4 blocks) per row: K <= 4096
 
 // ---- grouping ---------------------------------------------------------------------------
-// One workgroup. Positions inside an expert follow (token, slot) order, so the
-// result does not depend on thread timing.
+// One workgroup: count the (token, slot) entries of every expert, lay the experts out in
+// order (exp_off, tile_off), and give every entry a position inside its expert's range by
+// an LDS counter. The order of the entries inside an expert depends on timing, but nothing
+// computed from them does: each pair's GEMM column and epilogue depend on that pair alone,
+// and a token's pairs are combined in ascending expert order, which the ranges fix.
 __global__ __launch_bounds__(256) void k_group(const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                int P, int k, int E, int32_t* __restrict__ pair_tok,
                                                float* __restrict__ pair_w, int32_t* __restrict__ pair_of,
                                                int32_t* __restrict__ exp_off, int32_t* __restrict__ tile_off) {
   __shared__ int cnt[1024];
-  __shared__ int run[1024];
-  __shared__ int ce[256];
   const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 256) cnt[e] = 0, run[e] = 0;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
   __syncthreads();
-  for (int q = tid; q < P; q += 256) atomicAdd(&cnt[min(max(idx[q], 0), E - 1)], 1);
+  constexpr int kGJ = 8;  // entries per thread whose loads are issued together (one round trip)
+  for (int b0 = 0; b0 < P; b0 += 256 * kGJ) {
+    int ev[kGJ];
+#pragma unroll
+    for (int j = 0; j < kGJ; ++j) {
+      const int q = b0 + 256 * j + tid;
+      ev[j] = q < P ? min(max(idx[q], 0), E - 1) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kGJ; ++j)
+      if (ev[j] >= 0) atomicAdd(&cnt[ev[j]], 1);
+  }
   __syncthreads();
-  if (tid == 0) {
+  if (tid == 0) {  // expert offsets (serial over E <= 1024); cnt becomes the next free position
     int po = 0, to = 0;
     for (int e = 0; e < E; ++e) {
       exp_off[e] = po, tile_off[e] = to;
-      po += cnt[e], to += (cnt[e] + kPairTile - 1) / kPairTile;
-      cnt[e] = exp_off[e];  // reuse as the expert's base
+      const int c = cnt[e];
+      cnt[e] = po;
+      po += c, to += (c + kPairTile - 1) / kPairTile;
     }
     exp_off[E] = po, tile_off[E] = to;
   }
   __syncthreads();
-  for (int base = 0; base < P; base += 256) {
-    const int q = base + tid;
-    const int e = q < P ? min(max(idx[q], 0), E - 1) : -1;
-    ce[tid] = e;
-    __syncthreads();
-    if (e >= 0) {
-      int rank = 0;
-      for (int j = 0; j < tid; ++j) rank += ce[j] == e ? 1 : 0;
-      const int pos = cnt[e] + run[e] + rank;
-      pair_tok[pos] = q / k, pair_w[pos] = w[q], pair_of[q] = pos;
+  for (int b0 = 0; b0 < P; b0 += 256 * kGJ) {
+    int ev[kGJ];
+    float wv[kGJ];
+#pragma unroll
+    for (int j = 0; j < kGJ; ++j) {
+      const int q = b0 + 256 * j + tid;
+      ev[j] = q < P ? min(max(idx[q], 0), E - 1) : -1;
+      wv[j] = q < P ? w[q] : 0.f;
     }
-    __syncthreads();
-    if (e >= 0) atomicAdd(&run[e], 1);
-    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kGJ; ++j) {
+      if (ev[j] >= 0) {
+        const int q = b0 + 256 * j + tid;
+        const int pos = atomicAdd(&cnt[ev[j]], 1);
+        pair_tok[pos] = q / k, pair_w[pos] = wv[j], pair_of[q] = pos;
+      }
+    }
   }
 }
 
@@ -367,7 +383,9 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 
 // ---- combine -----------------------------------------------------------------------------
 // y[t][row] = sum over t's pairs in ascending pair index (= ascending expert) of
-// o[pair][row] + w * b_down[e][row]. One thread per (token, row).
+// o[pair][row] + w * b_down[e][row]. One thread per (token, row); the token's (at most KM)
+// pair indices stay in registers and are taken smallest first.
+template <int KM>
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, const int32_t* __restrict__ pair_of,
                                                  const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                  const float* __restrict__ down_b, int T, int k, int H,
@@ -375,18 +393,24 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, co
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long long)T * H) return;
   const int t = (int)(gid / H), row = (int)(gid % H);
-  int ps[16], ss[16];
-  for (int s = 0; s < k; ++s) {  // insertion sort of the token's pairs
-    const int p = pair_of[t * k + s];
-    int j = s;
-    while (j > 0 && ps[j - 1] > p) ps[j] = ps[j - 1], ss[j] = ss[j - 1], --j;
-    ps[j] = p, ss[j] = s;
-  }
+  int ps[KM];
+#pragma unroll
+  for (int s = 0; s < KM; ++s) ps[s] = s < k ? pair_of[t * k + s] : INT_MAX;
   float acc = 0.f;
-  for (int j = 0; j < k; ++j) {
-    float v = o[(size_t)ps[j] * H + row];
-    if (down_b) v = v + w[t * k + ss[j]] * down_b[(size_t)idx[t * k + ss[j]] * H + row];
-    acc = acc + v;
+#pragma unroll
+  for (int r = 0; r < KM; ++r) {
+    if (r < k) {
+      int best = INT_MAX, bs = 0;
+#pragma unroll
+      for (int s = 0; s < KM; ++s)
+        if (ps[s] < best) best = ps[s], bs = s;
+#pragma unroll
+      for (int s = 0; s < KM; ++s)
+        if (s == bs) ps[s] = INT_MAX;
+      float v = o[(size_t)best * H + row];
+      if (down_b) v = v + w[t * k + bs] * down_b[(size_t)idx[t * k + bs] * H + row];
+      acc = acc + v;
+    }
   }
   y[gid] = acc;
 }
@@ -499,8 +523,16 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   {
     ProfScope ps(K, "combine");
     const long long n = (long long)T * H;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w,
-                       L.d.down_bias, (int)T, k, H, y);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (k <= 4)
+      hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
+                         H, y);
+    else if (k <= 8)
+      hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
+                         H, y);
+    else
+      hipLaunchKernelGGL(k_combine<16>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
+                         H, y);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
