@@ -171,7 +171,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bst[kBBuf][kBStep];
   __shared__ __align__(16) uint32_t bsc[kBBuf][kPairTile * 4];
   __shared__ __align__(16) uint8_t ast[kGW][kGT * 16 * kARow];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches stay scalar
   const int i = lane & 15, g = lane >> 4;
   constexpr int kRows = GATEUP ? (kGW / 2) * kGT * 16 : kGW * kGT * 16;  // rows of a matrix per item
   // Work items are ordered (expert, row tile, pair tile of the expert), and each XCD
@@ -329,8 +330,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
             const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
             const int sb = (int)sc_base[srd + pg * 256 + 4 * k];
 #pragma unroll
-            for (int tt = 0; tt < kGT; ++tt)
-              if (tin[tt]) acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
+            for (int tt = 0; tt < kGT; ++tt)  // tiles past M repeat row M-1; their rows are not stored
+              acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
           }
         }
       }
