@@ -250,7 +250,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
   __shared__ __align__(16) int8_t hb[32];
   __shared__ float dn_part[kQ4MaxSlots][8];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches stay scalar
   const int bid = blockIdx.x;
   const int nsbH = a.H >> 8, nsbI = a.I >> 8, nGI = a.I >> 4;
   TRACE(0);
