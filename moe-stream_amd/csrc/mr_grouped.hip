@@ -302,40 +302,56 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     const uint8_t* bb_base = &bst[buf][0];
     const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
     const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
+    // A windows of block k (the 4 K groups of a row read the same window), read one block
+    // ahead of the MFMAs (windows of blocks past the row end stay inside the slice; their
+    // MFMAs are skipped). B is read next to its MFMAs.
+    struct Ops {
+      RawBlk r[kGT];
+    };
+    auto read_ops = [&](int k, Ops& o) {
+      const uint32_t wo = lead + 17u * (uint32_t)k;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (4 * st + k < nbK) {  // uniform: blocks past the row end are skipped
-        // A: window of block 4 st + k of this lane's row in each tile (the 4 K groups of a
-        // row read the same window)
-        const uint32_t wo = lead + 17u * (uint32_t)k;
-        const uint32_t t8 = 8u * ((wo & 3u) + 1u);
-        AOp ao[kGT];
-        int sa[kGT];
+      for (int tt = 0; tt < kGT; ++tt) {
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
+        o.r[tt].d[0] = wp[0], o.r[tt].d[1] = wp[1], o.r[tt].d[2] = wp[2], o.r[tt].d[3] = wp[3],
+        o.r[tt].d[4] = wp[4];
+      }
+    };
+    auto run_ops = [&](int k, const Ops& o) {
+      const uint32_t wo = lead + 17u * (uint32_t)k;
+      const uint32_t t8 = 8u * ((wo & 3u) + 1u);
+      AOp ao[kGT];
+      int sa[kGT];
 #pragma unroll
-        for (int tt = 0; tt < kGT; ++tt) {
-          const uint32_t* wp =
-              reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
-          RawBlk r;
-          r.d[0] = wp[0], r.d[1] = wp[1], r.d[2] = wp[2], r.d[3] = wp[3], r.d[4] = wp[4];
+      for (int tt = 0; tt < kGT; ++tt) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ao[tt].q[q] = (uint32_t)((((uint64_t)r.d[q + 1] << 32) | r.d[q]) >> t8);
-          sa[tt] = (int)((r.d[0] >> (8u * (wo & 3u))) & 0xFFu);
-        }
+        for (int q = 0; q < 4; ++q)
+          ao[tt].q[q] = (uint32_t)((((uint64_t)o.r[tt].d[q + 1] << 32) | o.r[tt].d[q]) >> t8);
+        sa[tt] = (int)((o.r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu);
+      }
 #pragma unroll
-        for (int pg = 0; pg < kPG; ++pg) {
-          if (pg < npg) {
-            const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
-            const i32x4 v0 = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
-            const i32x4 v1 = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
-            const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            const int sb = (int)sc_base[srd + pg * 256 + 4 * k];
+      for (int pg = 0; pg < kPG; ++pg) {
+        if (pg < npg) {
+          const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
+          const i32x4 v0 = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
+          const i32x4 v1 = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
+          const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          const int sb = (int)sc_base[srd + pg * 256 + 4 * k];
 #pragma unroll
-            for (int tt = 0; tt < kGT; ++tt)  // tiles past M repeat row M-1; their rows are not stored
-              acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
-          }
+          for (int tt = 0; tt < kGT; ++tt)  // tiles past M repeat row M-1; their rows are not stored
+            acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
         }
       }
-    }
+    };
+    Ops o0, o1;
+    read_ops(0, o0);
+    read_ops(1, o1);
+    if (4 * st + 0 < nbK) run_ops(0, o0);  // uniform: blocks past the row end are skipped
+    read_ops(2, o0);
+    if (4 * st + 1 < nbK) run_ops(1, o1);
+    read_ops(3, o1);
+    if (4 * st + 2 < nbK) run_ops(2, o0);
+    if (4 * st + 3 < nbK) run_ops(3, o1);
   };
   i32x4 apA[kAK], apB[kAK];
   BRegs bA, bB;
