@@ -282,31 +282,39 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     for (int h = 0; h < 2; ++h) brd[k][h] = b_slot(i, k, g + 4 * h) * 16;
   const int srd = i * 16 + g;  // scale byte of pair i, block 0, term g (block k: +4k; group: +256)
 
+  i32x4 apA[kAK], apB[kAK];
+  BRegs bR;
+  load_b(0, bR);
+  load_a(0, apA);
+  load_a(min(1, S - 1), apB);
+
   f32x4 acc[kGT][kPG];
 #pragma unroll
   for (int tt = 0; tt < kGT; ++tt)
 #pragma unroll
     for (int pg = 0; pg < kPG; ++pg) acc[tt][pg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Step st: pieces in register set st % 2, B in LDS buffer st % 2; the loads of step st + 2
-  // reuse the register set once it has been written to LDS.
-  // Every step issues the same loads (past the last step: the last step's data again), so
-  // the compiler's waits before the LDS writes count exactly one step's loads in flight.
-  auto step = [&](int st, i32x4 (&cur)[kAK], BRegs& bcur) {
+  // Step st: A pieces in register set st % 2 (loaded two steps ahead), B pieces in one
+  // register set (one step ahead: the images are L2 hits), B in LDS buffer st % 2. Every step
+  // issues the same loads, B first (past the last step: the last step's data again), so the
+  // compiler's waits before the LDS writes count exactly the loads issued after them.
+  auto step = [&](int st, i32x4 (&cur)[kAK]) {
     const int buf = st % kBBuf;
-    store_a(cur);        // this wave's A slice (its reads of step st-1 are done: LDS ops stay in order)
-    store_b(bcur, buf);  // buffer st % 2 was last read in step st-2, before the previous barrier
-    __syncthreads();     // step st's B stage is complete
-    load_b(min(st + 2, S - 1), bcur);
+    store_a(cur);      // this wave's A slice (its reads of step st-1 are done: LDS ops stay in order)
+    store_b(bR, buf);  // buffer st % 2 was last read in step st-2, before the previous barrier
+    __syncthreads();   // step st's B stage is complete
+    load_b(min(st + 1, S - 1), bR);
     load_a(min(st + 2, S - 1), cur);
     const uint8_t* bb_base = &bst[buf][0];
     const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
     const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
-    // A windows of block k (the 4 K groups of a row read the same window), read one block
-    // ahead of the MFMAs (windows of blocks past the row end stay inside the slice; their
-    // MFMAs are skipped). B is read next to its MFMAs.
+    // Operands of block k: the A windows of this lane's rows (the 4 K groups of a row read the
+    // same window) and the 2 pair groups' B, read one block ahead of the MFMAs (reads of blocks
+    // past the row end stay inside the LDS stages; their MFMAs are skipped).
     struct Ops {
       RawBlk r[kGT];
+      i32x4 b[kPG][2];
+      int sb[kPG];
     };
     auto read_ops = [&](int k, Ops& o) {
       const uint32_t wo = lead + 17u * (uint32_t)k;
@@ -315,6 +323,13 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
         o.r[tt].d[0] = wp[0], o.r[tt].d[1] = wp[1], o.r[tt].d[2] = wp[2], o.r[tt].d[3] = wp[3],
         o.r[tt].d[4] = wp[4];
+      }
+#pragma unroll
+      for (int pg = 0; pg < kPG; ++pg) {
+        const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
+        o.b[pg][0] = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
+        o.b[pg][1] = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
+        o.sb[pg] = (int)sc_base[srd + pg * 256 + 4 * k];
       }
     };
     auto run_ops = [&](int k, const Ops& o) {
@@ -332,14 +347,11 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 #pragma unroll
       for (int pg = 0; pg < kPG; ++pg) {
         if (pg < npg) {
-          const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
-          const i32x4 v0 = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
-          const i32x4 v1 = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
-          const i32x8 B = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          const int sb = (int)sc_base[srd + pg * 256 + 4 * k];
+          const i32x8 B = {o.b[pg][0][0], o.b[pg][0][1], o.b[pg][0][2], o.b[pg][0][3],
+                           o.b[pg][1][0], o.b[pg][1][1], o.b[pg][1][2], o.b[pg][1][3]};
 #pragma unroll
           for (int tt = 0; tt < kGT; ++tt)  // tiles past M repeat row M-1; their rows are not stored
-            acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, sb, acc[tt][pg]);
+            acc[tt][pg] = mfma_op(ao[tt], sa[tt], B, o.sb[pg], acc[tt][pg]);
         }
       }
     };
@@ -353,18 +365,12 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     if (4 * st + 2 < nbK) run_ops(2, o0);
     if (4 * st + 3 < nbK) run_ops(3, o1);
   };
-  i32x4 apA[kAK], apB[kAK];
-  BRegs bA, bB;
-  load_b(0, bA);
-  load_a(0, apA);
-  load_b(min(1, S - 1), bB);
-  load_a(min(1, S - 1), apB);
   int st = 0;
   for (; st + 1 < S; st += 2) {
-    step(st, apA, bA);
-    step(st + 1, apB, bB);
+    step(st, apA);
+    step(st + 1, apB);
   }
-  if (st < S) step(st, apA, bA);
+  if (st < S) step(st, apA);
 
   // Epilogue: acc[tt][pg][r] of lane (i, g) is row wrow0 + 16 tt + 4g + r x pair 16 pg + i.
   // The wave's block goes through LDS as [pair][row] so that each pair's rows are stored
