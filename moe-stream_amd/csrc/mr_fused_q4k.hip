@@ -69,8 +69,9 @@ constexpr int kDnVbuf = kDnHdec + 4 * kDnSbW * 64;          // [4][kDnSbW * 9] p
 constexpr int kDnEnd = kDnVbuf + 4 * kDnSbW * 9 * 4;
 constexpr int kQ4Smem = kGuEnd > kDnEnd ? kGuEnd : kDnEnd;
 static_assert(kDnSbW * 9 * 4 >= kDnSbW * 16, "raw headers fit in the partials slice");
-static_assert(72 * (kQ4MaxH / 256) <= 64 * kQ4GuIt && 72 * (kQ4MaxI / 256) <= 64 * kQ4DnIt,
-              "a wave's chunks cover its 8-row region");
+static_assert(kQ4MaxH / 256 <= 8 && kQ4GuIt == 9 && kQ4MaxI / 256 <= 3 && kQ4DnIt == 4,
+              "a wave's loads cover its 8-row region (chunk map: 9 loads for 8 super-blocks per row, "
+              "4 for up to 3)");
 static_assert(72 * (kQ4MaxH / 256) <= 576, "per-wave LDS slices hold a gate/up region");
 
 struct Q4Args {
@@ -117,25 +118,56 @@ __device__ __forceinline__ void split_i8(float v, float m, int& t0, int& t1, flo
 }
 
 // ---- regions: 8 rows of a Q4_K matrix each -------------------------------------------------
-// A wave holds ns regions (slots) of nsb super-blocks per row: nch = 72*nsb
-// chunks each; chunk c = 64*i + lane of region s is ch[s][i]. Work is split in
-// phases so a wave pays one LDS drain per phase for all its regions.
+// A region's chunk c = row * P + pos (P = 9 * nsb chunks per row, nsb <= 8) is held by one
+// (load j, lane) pair:
+//   nsb == 8:  loads j < 8 hold row j at pos = lane; load 8 holds row lane/8 at pos 64 + lane%8;
+//   nsb < 8:   rp = 64 / P rows per load; lane = h * P + pos holds row j * rp + h (lanes with
+//              h >= rp, and rows past 7, hold no chunk).
+// Each load is 1 KiB of consecutive bytes (nsb == 8, last load: 8 runs of 128 B), and a lane's
+// position is the same in every load but nsb == 8's last, so the activation operands of that
+// position are read from LDS once per region instead of once per chunk.
+struct QMap {
+  int rp, h, pos;  // rows per load, this lane's row within a load, its position
+  int trow, tpos;  // nsb == 8: row and position of the last load
+  bool wide;       // nsb == 8
+};
+__device__ __forceinline__ QMap q_map(int nsb) {
+  const int lane = threadIdx.x & 63;
+  QMap m;
+  m.wide = nsb == 8;
+  if (m.wide) {
+    m.rp = 1, m.h = 0, m.pos = lane, m.trow = lane >> 3, m.tpos = 64 + (lane & 7);
+  } else {
+    const int P = 9 * nsb;
+    m.rp = 64 / P, m.h = lane / P, m.pos = lane - m.h * P, m.trow = 8, m.tpos = m.pos;
+  }
+  return m;
+}
+// Row held by load j (8: none) and the position of that load.
+__device__ __forceinline__ int q_row(const QMap& m, int j) {
+  if (m.wide) return j < 8 ? j : m.trow;
+  return m.h < m.rp ? min(j * m.rp + m.h, 8) : 8;
+}
+__device__ __forceinline__ int q_pos(const QMap& m, int j) { return j == 8 ? m.tpos : m.pos; }
 
 // Phase 1 (needs only the weights): stage each super-block's header chunk in
 // LDS (hraw), then decode it into (d*sc_j, dmin*m_j) for its 8 sub-blocks (hdec,
 // 16 floats per super-block, regions one after another).
 template <int IT, int NS>
-__device__ __forceinline__ void region_headers(const uint4 (&ch)[NS][IT], int nsb, int ns, uint4* hraw,
-                                               float* hdec) {
+__device__ __forceinline__ void region_headers(const uint4 (&ch)[NS][IT], const QMap& m, int nsb, int ns,
+                                               uint4* hraw, float* hdec) {
   const int lane = threadIdx.x & 63;
-  const int nch = 72 * nsb, nsbr = 8 * nsb;
+  const int nsbr = 8 * nsb;
+  const int col = m.pos / 9;
+  const bool hpos = m.pos - 9 * col == 0;  // header chunks sit at positions 9 * col (never in the last
+                                           // load of nsb == 8: positions 64..71)
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
     if (r < ns) {
 #pragma unroll
-      for (int i = 0; i < IT; ++i) {
-        const int c = 64 * i + lane;
-        if (c < nch && c % 9 == 0) hraw[r * nsbr + c / 9] = ch[r][i];
+      for (int j = 0; j < IT; ++j) {
+        const int row = q_row(m, j);
+        if (j < 8 && hpos && row < 8) hraw[r * nsbr + row * nsb + col] = ch[r][j];
       }
     }
   }
@@ -159,79 +191,103 @@ __device__ __forceinline__ void region_headers(const uint4 (&ch)[NS][IT], int ns
   __builtin_amdgcn_wave_barrier();
 }
 
+// Activation operands of chunk position pos (quant chunk p = pos % 9 of super-block
+// column pos / 9): the int8 terms of its two 16-element groups (low nibbles: group G,
+// high nibbles: G + 2) and their (s0, group sum). Header positions (p == 0) read
+// position 1's operands; their products are discarded.
+struct XOps {
+  uint32_t l0[4], l1[4], h0[4], h1[4];
+  float2 gl, gh;
+  int hoff;  // float offset of the position's (d*sc, dmin*m) pairs within a super-block's 16
+  int col;
+  bool hdr;
+};
+__device__ __forceinline__ void x_ops(const uint8_t* xq, const float2* xs, int pos, XOps& o) {
+  const int col = pos / 9, p = pos - 9 * col;
+  o.hdr = p == 0;
+  const int pp = o.hdr ? 0 : p - 1, jj = pp >> 1, hf = pp & 1;
+  const int G = col * 16 + jj * 4 + hf;
+  const uint4 l0 = *reinterpret_cast<const uint4*>(xq + G * 32);
+  const uint4 l1 = *reinterpret_cast<const uint4*>(xq + G * 32 + 16);
+  const uint4 h0 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32);
+  const uint4 h1 = *reinterpret_cast<const uint4*>(xq + (G + 2) * 32 + 16);
+  o.l0[0] = l0.x, o.l0[1] = l0.y, o.l0[2] = l0.z, o.l0[3] = l0.w;
+  o.l1[0] = l1.x, o.l1[1] = l1.y, o.l1[2] = l1.z, o.l1[3] = l1.w;
+  o.h0[0] = h0.x, o.h0[1] = h0.y, o.h0[2] = h0.z, o.h0[3] = h0.w;
+  o.h1[0] = h1.x, o.h1[1] = h1.y, o.h1[2] = h1.z, o.h1[3] = h1.w;
+  o.gl = xs[G], o.gh = xs[G + 2];
+  o.hoff = 4 * jj, o.col = col;
+}
+
+// One quant chunk (16 low nibbles of sub-block 2jj, 16 high nibbles of sub-block 2jj+1)
+// against its activation operands: per half, (d*sc) * (s0*A0 + s1*A1) - (dmin*m) * sum.
+__device__ __forceinline__ float chunk_dot(const uint4& wc, const XOps& o, const float4& dm) {
+  const uint32_t w[4] = {wc.x, wc.y, wc.z, wc.w};
+  int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int lo = (int)(w[d] & 0x0F0F0F0Fu), hi = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
+    a0 = __builtin_amdgcn_sdot4(lo, (int)o.l0[d], a0, false);
+    a1 = __builtin_amdgcn_sdot4(lo, (int)o.l1[d], a1, false);
+    b0 = __builtin_amdgcn_sdot4(hi, (int)o.h0[d], b0, false);
+    b1 = __builtin_amdgcn_sdot4(hi, (int)o.h1[d], b1, false);
+  }
+  const float xlo = o.gl.x * (float)a0 + (o.gl.x * kInv254) * (float)a1;
+  const float xhi = o.gh.x * (float)b0 + (o.gh.x * kInv254) * (float)b1;
+  return ((dm.x * xlo - dm.y * o.gl.y) + dm.z * xhi) - dm.w * o.gh.y;
+}
+
 // Phase 2: quant-chunk dot products against the activation images (xq[r]: [G][32 B]
-// int8 terms, xs[r]: [G] (s0, group sum)) into vbuf, then each row's sum; out[r]
-// is left in lanes 8*row (row = 0..7). vbuf may alias hraw (headers are decoded).
+// int8 terms, xs[r]: [G] (s0, group sum)) into vbuf (chunk order), then each row's sum;
+// out[r] is left in lanes 8*row (row = 0..7). vbuf may alias hraw (headers are decoded).
+// Header chunks and lanes without a chunk write 0 (the latter to chunk 0, a header).
 template <int IT, int NS>
-__device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], int nsb, int ns,
+__device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], const QMap& m, int nsb, int ns,
                                             const uint8_t* const (&xq)[NS], const float2* const (&xs)[NS],
                                             const float* hdec, float* vbuf, float (&out)[NS]) {
   const int lane = threadIdx.x & 63;
-  const int nch = 72 * nsb, nsbr = 8 * nsb;
-  // sbw / nsb for sbw < 64 as a multiply: (sbw * ceil(2^16 / nsb)) >> 16 is exact there
-  const uint32_t inv_nsb = (65536u + (uint32_t)nsb - 1u) / (uint32_t)nsb;
+  const int P = 9 * nsb, nch = 8 * P, nsbr = 8 * nsb;
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
     if (r < ns) {
+      XOps xm, xt;
+      x_ops(xq[r], xs[r], m.pos, xm);
+      if (IT > 8) x_ops(xq[r], xs[r], m.tpos, xt);
 #pragma unroll
-      for (int i = 0; i < IT; ++i) {
-        const int c = 64 * i + lane;
-        if (c < nch) {
-          const int sbw = c / 9, p = c - 9 * sbw;
-          float v = 0.f;
-          if (p != 0) {
-            const int col = sbw - (int)(((uint32_t)sbw * inv_nsb) >> 16) * nsb;
-            const int pp = p - 1, jj = pp >> 1, hf = pp & 1;
-            const int G = col * 16 + jj * 4 + hf;  // low nibbles; high nibbles: G + 2
-            const uint4 l0 = *reinterpret_cast<const uint4*>(xq[r] + G * 32);
-            const uint4 l1 = *reinterpret_cast<const uint4*>(xq[r] + G * 32 + 16);
-            const uint4 h0 = *reinterpret_cast<const uint4*>(xq[r] + (G + 2) * 32);
-            const uint4 h1 = *reinterpret_cast<const uint4*>(xq[r] + (G + 2) * 32 + 16);
-            const uint32_t w[4] = {ch[r][i].x, ch[r][i].y, ch[r][i].z, ch[r][i].w};
-            const uint32_t xl0[4] = {l0.x, l0.y, l0.z, l0.w}, xl1[4] = {l1.x, l1.y, l1.z, l1.w};
-            const uint32_t xh0[4] = {h0.x, h0.y, h0.z, h0.w}, xh1[4] = {h1.x, h1.y, h1.z, h1.w};
-            int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              const int lo = (int)(w[d] & 0x0F0F0F0Fu), hi = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
-              a0 = __builtin_amdgcn_sdot4(lo, (int)xl0[d], a0, false);
-              a1 = __builtin_amdgcn_sdot4(lo, (int)xl1[d], a1, false);
-              b0 = __builtin_amdgcn_sdot4(hi, (int)xh0[d], b0, false);
-              b1 = __builtin_amdgcn_sdot4(hi, (int)xh1[d], b1, false);
-            }
-            const float2 gl = xs[r][G], gh = xs[r][G + 2];
-            const float4 dm = *reinterpret_cast<const float4*>(hdec + (r * nsbr + sbw) * 16 + 4 * jj);
-            const float xlo = gl.x * (float)a0 + (gl.x * kInv254) * (float)a1;
-            const float xhi = gh.x * (float)b0 + (gh.x * kInv254) * (float)b1;
-            v = ((dm.x * xlo - dm.y * gl.y) + dm.z * xhi) - dm.w * gh.y;
-          }
-          vbuf[r * nch + c] = v;
-        }
+      for (int j = 0; j < IT; ++j) {
+        const XOps& o = j < 8 ? xm : xt;
+        const int row = q_row(m, j);
+        const bool ok = row < 8 && !o.hdr;
+        const int sb = min(row, 7) * nsb + o.col;
+        const float4 dm = *reinterpret_cast<const float4*>(hdec + (r * nsbr + sb) * 16 + o.hoff);
+        const float v = chunk_dot(ch[r][j], o, dm);
+        vbuf[r * nch + (row < 8 ? row * P + q_pos(m, j) : 0)] = ok ? v : 0.f;
       }
     }
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
   // row sums: 8 lanes per row, each over every 8th chunk of the row, then DPP
-  const int row = lane >> 3, j8 = lane & 7, per = 9 * nsb;
+  const int row = lane >> 3, j8 = lane & 7;
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
     float sm = 0.f;
     if (r < ns)
-      for (int c = j8; c < per; c += 8) sm += vbuf[r * nch + row * per + c];
+      for (int c = j8; c < P; c += 8) sm += vbuf[r * nch + row * P + c];
     out[r] = sum8(sm);
   }
 }
 
-// Loads of one region (8 rows x nsb super-blocks at `base`); chunks past the end
-// load the last chunk (ignored).
+// Loads of one region (8 rows x nsb super-blocks at `base`); a lane without a chunk in a
+// load reads chunk 0 (ignored).
 template <int IT>
-__device__ __forceinline__ void region_load(const uint8_t* base, int nsb, uint4 (&ch)[IT]) {
-  const int lane = threadIdx.x & 63, nch = 72 * nsb;
+__device__ __forceinline__ void region_load(const uint8_t* base, const QMap& m, int nsb, uint4 (&ch)[IT]) {
+  const int P = 9 * nsb;
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = min(64 * i + lane, nch - 1);
-    ch[i] = *reinterpret_cast<const uint4*>(base + (size_t)c * 16);
+  for (int j = 0; j < IT; ++j) {
+    const int row = q_row(m, j);
+    const int c = row < 8 ? row * P + q_pos(m, j) : 0;
+    ch[j] = *reinterpret_cast<const uint4*>(base + (size_t)c * 16);
   }
 }
 
@@ -362,8 +418,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const int e = sh ? 0 : sel_i[slot];
       const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e);
       const size_t rb = (size_t)nsbH * 144;
+      const QMap qm = q_map(nsbH);
       uint4 ch[1][kQ4GuIt];
-      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, nsbH, ch[0]);
+      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, qm, nsbH, ch[0]);
       if (wave == 0) {  // routing weights (and the shared expert's sigmoid gate) while the rows load
         route_finish(rc, rs, sel_w, sel_o);
         if (a.has_sh && lane == 0) {
@@ -379,12 +436,12 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         if (a.up_b) ubias = a.up_b[bi];
       }
       float* hdec = reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16;
-      region_headers<kQ4GuIt, 1>(ch, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
+      region_headers<kQ4GuIt, 1>(ch, qm, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
       XTRACE(wave);  // per wave: weights landed, headers decoded
       const uint8_t* const xqs[1] = {xq};
       const float2* const xss[1] = {xs};
       float r[1];
-      region_dots<kQ4GuIt, 1>(ch, nsbH, 1, xqs, xss, hdec, reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576, r);
+      region_dots<kQ4GuIt, 1>(ch, qm, nsbH, 1, xqs, xss, hdec, reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576, r);
       XTRACE(4 + wave);  // per wave: dot products done
       if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r[0];
       TRACE(3);
@@ -428,13 +485,14 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
     TRACE(1);
     if (ok_flag) {
       const size_t rb = (size_t)nsbI * 144;
+      const QMap qm = q_map(nsbI);
       uint4 ch[kQ4DnSlots][kQ4DnIt];
 #pragma unroll
       for (int j = 0; j < kQ4DnSlots; ++j) {
         const int s = wave + 4 * j;
         const int sc = s < a.ktot ? s : 0;
         const uint8_t* D = sc >= a.k ? a.sh_down : expert_at(a.down, sel_i[sc]);
-        if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, nsbI, ch[j]);
+        if (s < a.ktot) region_load<kQ4DnIt>(D + (size_t)(q * 8) * rb, qm, nsbI, ch[j]);
       }
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       const float yres = (tid < 8 && NORM && q * 8 + tid < a.H) ? a.nr.resid[q * 8 + tid] : 0.f;
@@ -445,7 +503,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const int nsw = (a.ktot - wave + 3) >> 2;  // slots of this wave: wave, wave + 4, ...
       float* hdec = reinterpret_cast<float*>(smem + kDnHdec) + wave * kDnSbW * 16;
       float* vbuf = reinterpret_cast<float*>(smem + kDnVbuf) + wave * kDnSbW * 9;
-      region_headers<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, reinterpret_cast<uint4*>(vbuf), hdec);
+      region_headers<kQ4DnIt, kQ4DnSlots>(ch, qm, nsbI, nsw, reinterpret_cast<uint4*>(vbuf), hdec);
       TRACE(2);
       if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit,
                                                          (uint32_t)a.NG / 4) && lane == 0)
@@ -482,7 +540,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
           xqs[j] = hq + (size_t)sj * nGI * 32, xss[j] = hs + (size_t)sj * nGI;
         }
         float r[kQ4DnSlots];
-        region_dots<kQ4DnIt, kQ4DnSlots>(ch, nsbI, nsw, xqs, xss, hdec, vbuf, r);
+        region_dots<kQ4DnIt, kQ4DnSlots>(ch, qm, nsbI, nsw, xqs, xss, hdec, vbuf, r);
 #pragma unroll
         for (int j = 0; j < kQ4DnSlots; ++j)
           if (j < nsw && (lane & 7) == 0) dn_part[wave + 4 * j][lane >> 3] = r[j];
