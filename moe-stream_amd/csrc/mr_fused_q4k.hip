@@ -54,8 +54,7 @@ constexpr float kInv254 = 1.0f / 254.0f;
 // LDS carve-up (bytes), gate/up workgroups
 constexpr int kGuXq = 0;                                 // [H/16][2 x 16 int8] x terms
 constexpr int kGuXs = kGuXq + kQ4MaxH * 2;               // [H/16] float2 (s0, group sum)
-constexpr int kGuHraw = kGuXs + kQ4MaxH / 16 * 8;        // [4 waves][64 sb] raw headers
-constexpr int kGuHdec = kGuHraw + 4 * 64 * 16;           // [4][64 sb][16 floats] decoded
+constexpr int kGuHdec = kGuXs + kQ4MaxH / 16 * 8;        // [4 waves][64 sb][16 floats] decoded headers
 constexpr int kGuVbuf = kGuHdec + 4 * 64 * 64;           // [4][576] chunk partials
 constexpr int kGuEnd = kGuVbuf + 4 * 576 * 4;
 // down workgroups. A wave takes ns = ceil(ktot/4) slots; per-wave header and
@@ -150,6 +149,22 @@ __device__ __forceinline__ int q_row(const QMap& m, int j) {
 }
 __device__ __forceinline__ int q_pos(const QMap& m, int j) { return j == 8 ? m.tpos : m.pos; }
 
+// A super-block header (d, dmin, 12 scale bytes) decoded into (d*sc_j, dmin*m_j) for its
+// 8 sub-blocks: 16 floats at out.
+__device__ __forceinline__ void header_decode(const uint4& h, float* out16) {
+  const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+  const uint32_t s3[3] = {h.y, h.z, h.w};
+  float4* out = reinterpret_cast<float4*>(out16);
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    uint32_t sc0, m0, sc1, m1;
+    q4k_scale_min((uint32_t)j, s3, sc0, m0);
+    q4k_scale_min((uint32_t)j + 1u, s3, sc1, m1);
+    out[j / 2] = float4{__fmul_rn(d, (float)sc0), __fmul_rn(dmin, (float)m0),
+                        __fmul_rn(d, (float)sc1), __fmul_rn(dmin, (float)m1)};
+  }
+}
+
 // Phase 1 (needs only the weights): stage each super-block's header chunk in
 // LDS (hraw), then decode it into (d*sc_j, dmin*m_j) for its 8 sub-blocks (hdec,
 // 16 floats per super-block, regions one after another).
@@ -173,22 +188,18 @@ __device__ __forceinline__ void region_headers(const uint4 (&ch)[NS][IT], const 
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
-  for (int b = lane; b < ns * nsbr; b += 64) {
-    const uint4 h = hraw[b];
-    const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
-    const uint32_t s3[3] = {h.y, h.z, h.w};
-    float4* out = reinterpret_cast<float4*>(hdec + b * 16);
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      uint32_t sc0, m0, sc1, m1;
-      q4k_scale_min((uint32_t)j, s3, sc0, m0);
-      q4k_scale_min((uint32_t)j + 1u, s3, sc1, m1);
-      out[j / 2] = float4{__fmul_rn(d, (float)sc0), __fmul_rn(dmin, (float)m0),
-                          __fmul_rn(d, (float)sc1), __fmul_rn(dmin, (float)m1)};
-    }
-  }
+  for (int b = lane; b < ns * nsbr; b += 64) header_decode(hraw[b], hdec + b * 16);
   lds_drain();
   __builtin_amdgcn_wave_barrier();
+}
+
+// Header of a region's super-block lane (row lane / nsb, column lane % nsb), for lanes
+// below 8 * nsb, as one load issued ahead of the region's chunks: it lands first, so the
+// headers decode while the chunks stream in.
+__device__ __forceinline__ uint4 region_header_load(const uint8_t* base, int nsb) {
+  const int lane = threadIdx.x & 63;
+  const int b = min(lane, 8 * nsb - 1), row = b / nsb;
+  return *reinterpret_cast<const uint4*>(base + (size_t)row * nsb * 144 + (size_t)(b - row * nsb) * 144);
 }
 
 // Activation operands of chunk position pos (quant chunk p = pos % 9 of super-block
@@ -267,13 +278,19 @@ __device__ __forceinline__ void region_dots(const uint4 (&ch)[NS][IT], const QMa
   }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
-  // row sums: 8 lanes per row, each over every 8th chunk of the row, then DPP
+  // row sums: 8 lanes per row, each over every 8th chunk of the row (at most IT: P <= 8 * IT),
+  // then DPP; the reads are issued together
   const int row = lane >> 3, j8 = lane & 7;
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
     float sm = 0.f;
-    if (r < ns)
-      for (int c = j8; c < P; c += 8) sm += vbuf[r * nch + row * P + c];
+    if (r < ns) {
+      float e[IT];
+#pragma unroll
+      for (int t = 0; t < IT; ++t) e[t] = j8 + 8 * t < P ? vbuf[r * nch + row * P + j8 + 8 * t] : 0.f;
+#pragma unroll
+      for (int t = 0; t < IT; ++t) sm += e[t];
+    }
     out[r] = sum8(sm);
   }
 }
@@ -419,30 +436,31 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
       const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e);
       const size_t rb = (size_t)nsbH * 144;
       const QMap qm = q_map(nsbH);
-      uint4 ch[1][kQ4GuIt];
-      region_load<kQ4GuIt>(W + (size_t)(urow * 16 + half * 8) * rb, qm, nsbH, ch[0]);
-      if (wave == 0) {  // routing weights (and the shared expert's sigmoid gate) while the rows load
-        route_finish(rc, rs, sel_w, sel_o);
-        if (a.has_sh && lane == 0) {
-          const float z = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
-          sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(z) : 1.f;
-        }
-      }
-      // the epilogue's biases (wave 0, lanes < 16), loaded before the dot products
-      float gbias = 0.f, ubias = 0.f;
-      if (wave == 0 && lane < 16 && !sh) {
+      const uint8_t* Wr = W + (size_t)(urow * 16 + half * 8) * rb;
+      // loads used only by the epilogue issue first: a wait for the region's header (the next
+      // load) or for its chunks then never waits for them
+      float zsh = 0.f, gbias = 0.f, ubias = 0.f;
+      if (wave == 0 && a.has_sh && lane == 0) zsh = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
+      if (wave == 0 && lane < 16 && !sh) {  // the epilogue's biases
         const size_t bi = (size_t)e * a.I + urow * 16 + lane;
         if (a.gate_b) gbias = a.gate_b[bi];
         if (a.up_b) ubias = a.up_b[bi];
       }
+      const uint4 hdr = region_header_load(Wr, nsbH);
+      uint4 ch[1][kQ4GuIt];
+      region_load<kQ4GuIt>(Wr, qm, nsbH, ch[0]);
+      if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // routing weights while the rows load
       float* hdec = reinterpret_cast<float*>(smem + kGuHdec) + wave * 64 * 16;
-      region_headers<kQ4GuIt, 1>(ch, qm, nsbH, 1, reinterpret_cast<uint4*>(smem + kGuHraw) + wave * 64, hdec);
+      if (lane < 8 * nsbH) header_decode(hdr, hdec + lane * 16);
+      lds_drain();
+      __builtin_amdgcn_wave_barrier();
       XTRACE(wave);  // per wave: weights landed, headers decoded
       const uint8_t* const xqs[1] = {xq};
       const float2* const xss[1] = {xs};
       float r[1];
       region_dots<kQ4GuIt, 1>(ch, qm, nsbH, 1, xqs, xss, hdec, reinterpret_cast<float*>(smem + kGuVbuf) + wave * 576, r);
       XTRACE(4 + wave);  // per wave: dot products done
+      if (wave == 0 && a.has_sh && lane == 0) sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(zsh) : 1.f;
       if ((lane & 7) == 0) gu_part[mat][half * 8 + (lane >> 3)] = r[0];
       TRACE(3);
       __syncthreads();
