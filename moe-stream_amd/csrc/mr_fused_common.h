@@ -336,10 +336,13 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 // The k-th largest key of the wave's NJ key columns: the largest T with at least k
 // keys >= T, fixed one bit at a time from the top (per bit, one ballot per column; the
 // compares issue before the first scalar count reads a mask). A lone wave issues about
-// one instruction per four cycles, so fewer instructions per bit beat fewer steps.
+// one instruction per four cycles, so fewer instructions per bit beat fewer steps. Once
+// exactly k keys are >= the prefix, the k-th largest is the least of them: one wave
+// minimum ends the search (for spread-out logits, after about half of the 32 bits).
 template <int NJ>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[kRouteVals], int k) {
   uint32_t T = 0u;
+  bool exact = false;
 #pragma unroll
   for (int b = 31; b >= 0; --b) {
     const uint32_t t = T | (1u << b);
@@ -351,7 +354,19 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[kRouteVals], i
     for (int j = 0; j < NJ; ++j) c += __popcll(m[j]);
     __builtin_amdgcn_sched_group_barrier(0x2, NJ, 0);
     __builtin_amdgcn_sched_group_barrier(0x4, 2 * NJ + 3, 0);
-    T = c >= k ? t : T;
+    if (c >= k) {
+      T = t;
+      if (c == k) {  // wave-uniform
+        exact = true;
+        break;
+      }
+    }
+  }
+  if (exact) {
+    uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mn = key[j] >= T ? min(mn, key[j]) : mn;
+    T = wave_min_u(mn);
   }
   return T;
 }
