@@ -105,7 +105,7 @@ int upload_offsets(mr_ctx* c, mr_pack* p) {
 
 // Scratch layout for T tokens of a layer shape.
 struct ScratchPlan {
-  uint64_t idx, w, logits, act, act_sh, mfma_b, sync, groups, grouped, xn, ytmp, total;
+  uint64_t idx, w, logits, rpart, act, act_sh, mfma_b, sync, groups, grouped, xn, ytmp, total;
 };
 
 ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
@@ -114,6 +114,7 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.idx = o, o += align_up(T * k * 4);
   p.w = o, o += align_up(T * k * 4);
   p.logits = o, o += align_up(T * E * 4);
+  p.rpart = o, o += align_up(4 * T * E * 4);
   p.act = o, o += align_up(T * k * I * 4);
   p.act_sh = o, o += align_up(T * (Ish + 1) * 4);
   // MFMA B-operand images: x split (H/32 blocks) and act split (k*I/32 blocks),
@@ -161,6 +162,7 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   s.idx = reinterpret_cast<int32_t*>(b + p.idx);
   s.w = reinterpret_cast<float*>(b + p.w);
   s.logits = reinterpret_cast<float*>(b + p.logits);
+  s.rpart = reinterpret_cast<float*>(b + p.rpart);
   s.act = reinterpret_cast<float*>(b + p.act);
   s.act_sh = reinterpret_cast<float*>(b + p.act_sh);
   s.mfma_b = b + p.mfma_b;
@@ -577,8 +579,7 @@ int mr_router_topk(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, int
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
   float* lg = logits ? logits : c->scratch.logits;
-  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, T, lg);
-  if (e == hipSuccess) e = mr::launch_topk(c->launch(), lg, T, L->E, L->d.top_k, L->d.route_flags, idx, w);
+  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, lg, c->scratch.rpart, idx, w);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "router launch");
 }
 
@@ -683,8 +684,7 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
   mr::Scratch& s = c->scratch;
-  hipError_t e = mr::launch_router_logits(c->launch(), *L, x, T, s.logits);
-  if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, T, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
+  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, s.logits, s.rpart, s.idx, s.w);
   if (e == hipSuccess) {
     if (c->decode_kernel != MR_DECODE_VALU && mr::grouped_supported(*L))
       e = mr::launch_grouped(c->launch(), *L, x, T, s.idx, s.w, y,

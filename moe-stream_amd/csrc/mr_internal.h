@@ -25,6 +25,7 @@ struct Scratch {
   int32_t* idx = nullptr;      // [T, k]
   float* w = nullptr;          // [T, k]
   float* logits = nullptr;     // [T, E]
+  float* rpart = nullptr;      // [4, T, E] router partial sums
   float* act = nullptr;        // [T, k, I] or grouped [T*k, I]
   float* act_sh = nullptr;     // [T, Ish] shared expert activation
   void* mfma_b = nullptr;      // MFMA B-operand images (x split / act split)
@@ -147,6 +148,9 @@ namespace mr {
 hipError_t launch_zero(const Launch& L, void* dst, uint64_t nbytes);
 hipError_t launch_router_logits(const Launch& K, const mr_layer& L, const float* x, uint32_t T,
                                 float* logits);
+// Router logits (written to logits) and top-k for T tokens; part: [4][T][E] floats of scratch.
+hipError_t launch_router_topk(const Launch& K, const mr_layer& L, const float* x, uint32_t T, float* logits,
+                              float* part, int32_t* idx, float* w);
 hipError_t launch_topk(const Launch& K, const float* logits, uint32_t T, uint32_t E, uint32_t k,
                        uint32_t flags, int32_t* idx, float* w);
 hipError_t launch_experts_valu(const Launch& K, const mr_layer& L, const float* x, uint32_t T,

@@ -59,10 +59,72 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
   }
 }
 
+// Router GEMM for many tokens on the fp32 MFMA (v_mfma_f32_16x16x4f32): a 1024-thread
+// workgroup takes 16 tokens x 16 experts x one of nks ranges of H's 16-element blocks; its
+// 16 waves take the range's blocks in turn (wave w: blocks w, w+16, ...), each issuing all of
+// its loads before its first MFMA, and the 16 partial tiles are summed in LDS in wave order.
+// A CU reaches only a fraction of HBM bandwidth with its own loads, so H is split over
+// workgroups until the grid spans the CUs (k_router_topk_finish adds the nks partials in
+// order: the same bits on every run). MFMA operands: lane (i, g) = lane % 16, lane / 16 holds
+// x[t0+i][k..k+3] and Wr[e0+i][k..k+3] for k = 16b + 4g, and MFMA j of the block multiplies
+// their element j, so the four MFMAs cover the block's 16 elements; D[4g + r][i] is token
+// t0+4g+r, expert e0+i. Tokens past T and experts past E repeat the last row (not stored).
+// part: [nks][T][E]. H % 4 == 0 and ceil(H/16) <= nks * 16 * kRouterBlocks.
+constexpr int kRouterWaves = 16, kRouterBlocks = 6, kRouterMaxSplit = 4;
+__global__ __launch_bounds__(1024) void k_router_logits_mfma(const float* __restrict__ x,
+                                                             const float* __restrict__ wr,
+                                                             float* __restrict__ part, int T, int H, int E,
+                                                             int nks) {
+  __shared__ f32x4 red[kRouterWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  const int nb = (H + 15) >> 4, per = (nb + nks - 1) / nks;
+  const int kb0 = (int)blockIdx.z * per, kb1 = min(nb, kb0 + per);
+  const float* xr = x + (size_t)min(t0 + i, T - 1) * H + 4 * g;
+  const float* wrow = wr + (size_t)min(e0 + i, E - 1) * H + 4 * g;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 a[kRouterBlocks], w[kRouterBlocks];
+#pragma unroll
+  for (int j = 0; j < kRouterBlocks; ++j) {
+    const int b = kb0 + wave + kRouterWaves * j;
+    const bool in = b < kb1 && 16 * b + 4 * g < H;
+    a[j] = in ? *reinterpret_cast<const f32x4*>(xr + 16 * b) : z;
+    w[j] = in ? *reinterpret_cast<const f32x4*>(wrow + 16 * b) : z;
+  }
+  f32x4 acc = z;
+#pragma unroll
+  for (int j = 0; j < kRouterBlocks; ++j) {
+    if (kb0 + wave + kRouterWaves * j < kb1) {  // wave-uniform
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, w[j].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, w[j].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, w[j].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, w[j].w, acc, 0, 0, 0);
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 s = red[0][lane];
+#pragma unroll
+    for (int q = 1; q < kRouterWaves; ++q) {
+      const f32x4 p = red[q][lane];
+      s = f32x4{s[0] + p[0], s[1] + p[1], s[2] + p[2], s[3] + p[3]};
+    }
+    const int e = e0 + i;
+    float* out = part + (size_t)blockIdx.z * T * E;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 4 * g + r;
+      if (t < T && e < E) out[(size_t)t * E + e] = s[r];
+    }
+  }
+}
+
 hipError_t launch_router_logits(const Launch& K, const mr_layer& L, const float* x, uint32_t T,
                                 float* logits) {
-  dim3 grid((L.E + 3) / 4, T);
   ProfScope ps(K, "router_logits");
+  dim3 grid((L.E + 3) / 4, T);
   hipLaunchKernelGGL(k_router_logits, grid, dim3(256), 0, K.s, x, L.d.router_w, L.d.router_b,
                      L.d.dummy_mask, logits, (int)L.H, (int)L.E);
   return hipGetLastError();
@@ -83,17 +145,10 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
-__device__ void topk_wave(const float* row, int E, int k, uint32_t flags, int32_t* out_idx,
+// Top-k of the logits v[j] of experts lane + 64 j (live[j]: e < E).
+__device__ void topk_vals(float (&v)[8], bool (&live)[8], int k, uint32_t flags, int32_t* out_idx,
                           float* out_w, float* sel_v /* LDS [16] */, int* sel_i /* LDS [16] */) {
   const int lane = threadIdx.x & 63;
-  float v[8];
-  bool live[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    int e = lane + 64 * j;
-    live[j] = e < E;
-    v[j] = live[j] ? row[e] : 0.f;
-  }
   const bool softmax_after = (flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
   float mx_all = 0.f, sum_all = 0.f;
   if (!softmax_after) {
@@ -147,6 +202,72 @@ __device__ void topk_wave(const float* row, int E, int k, uint32_t flags, int32_
     }
     for (int r = 0; r < k; ++r) out_idx[r] = sel_i[r];
   }
+}
+
+__device__ void topk_wave(const float* row, int E, int k, uint32_t flags, int32_t* out_idx,
+                          float* out_w, float* sel_v /* LDS [16] */, int* sel_i /* LDS [16] */) {
+  const int lane = threadIdx.x & 63;
+  float v[8];
+  bool live[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int e = lane + 64 * j;
+    live[j] = e < E;
+    v[j] = live[j] ? row[e] : 0.f;
+  }
+  topk_vals(v, live, k, flags, out_idx, out_w, sel_v, sel_i);
+}
+
+// Router logits from the H-split partials of k_router_logits_mfma (summed in split order,
+// then + bias + mask, the order of k_router_logits), written to logits, then the top-k.
+__global__ __launch_bounds__(64) void k_router_topk_finish(const float* __restrict__ part, int nks, int T,
+                                                           const float* __restrict__ br,
+                                                           const float* __restrict__ mask,
+                                                           float* __restrict__ logits, int E, int k,
+                                                           uint32_t flags, int32_t* __restrict__ idx,
+                                                           float* __restrict__ w) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int t = blockIdx.x, lane = threadIdx.x & 63;
+  float v[8];
+  bool live[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    live[j] = e < E;
+    float s = 0.f;
+    if (live[j]) {
+      s = part[(size_t)t * E + e];
+      for (int q = 1; q < nks; ++q) s = s + part[((size_t)q * T + t) * E + e];
+      if (br) s = s + br[e];
+      if (mask) s = s + mask[e];
+      logits[(size_t)t * E + e] = s;
+    }
+    v[j] = s;
+  }
+  topk_vals(v, live, k, flags, idx + (size_t)t * k, w + (size_t)t * k, sv, si);
+}
+
+hipError_t launch_router_topk(const Launch& K, const mr_layer& L, const float* x, uint32_t T, float* logits,
+                              float* part, int32_t* idx, float* w) {
+  const uint32_t nb = (L.H + 15) / 16, tiles = ((L.E + 15) / 16) * ((T + 15) / 16);
+  uint32_t nks = std::max<uint32_t>((nb + 16 * kRouterBlocks - 1) / (16 * kRouterBlocks), (256 + tiles - 1) / tiles);
+  nks = std::min<uint32_t>(nks, kRouterMaxSplit);
+  if (T < 16 || L.H % 4 != 0 || nb > nks * 16u * kRouterBlocks) {
+    hipError_t e = launch_router_logits(K, L, x, T, logits);
+    return e == hipSuccess ? launch_topk(K, logits, T, L.E, L.d.top_k, L.d.route_flags, idx, w) : e;
+  }
+  {
+    ProfScope ps(K, "router_logits");
+    hipLaunchKernelGGL(k_router_logits_mfma, dim3((L.E + 15) / 16, (T + 15) / 16, nks), dim3(64 * kRouterWaves), 0,
+                       K.s, x, L.d.router_w, part, (int)T, (int)L.H, (int)L.E, (int)nks);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  ProfScope ps(K, "topk");
+  hipLaunchKernelGGL(k_router_topk_finish, dim3(T), dim3(64), 0, K.s, part, (int)nks, (int)T, L.d.router_b,
+                     L.d.dummy_mask, logits, (int)L.E, (int)L.d.top_k, L.d.route_flags, idx, w);
+  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, int E, int k,

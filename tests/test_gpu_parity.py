@@ -145,12 +145,12 @@ def test_forward_decode_parity(gpu_ctx, layers, name):
         dx.free(), dy.free()
 
 
+@pytest.mark.parametrize("T", [8, 40])  # 40: the 16x16-tile MFMA router GEMM with ragged tiles
 @pytest.mark.parametrize("name", list(SPECS))
-def test_router_topk_parity(gpu_ctx, layers, name):
+def test_router_topk_parity(gpu_ctx, layers, name, T):
     dl, host = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
     L = oracle.layer_from_host(host)
-    T = 8
     x = W.x_tokens(spec, T, first_token=10)
     dx = gpu_ctx.to_device(x)
     di, dw, dlg = gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.n_experts * 4)
