@@ -6,11 +6,12 @@
 // (layer.rs:2148-2183; CPU: mxfp4_matmul per expert, layer.rs:1449-1514). Here:
 //   k_group       (token, slot) pairs grouped by expert; per-expert pair offsets and
 //                 32-pair tile offsets; pair index of every (token, slot).
-//   k_split_rows  activation rows -> e4m3 B images (4 terms per 32-element block).
-//   k_grouped_gemm<true>   gate and up for one (expert, 64-row tile, 32-pair tile):
-//                 A = native MXFP4 weight rows, B = the 16 pairs' x images; epilogue
-//                 bias + activation x routing weight -> h [pair][I].
-//   k_grouped_gemm<false>  down for one (expert, 128-row tile, 32-pair tile) on the
+//   k_split_rows  x rows -> e4m3 B images (4 terms per 32-element block).
+//   k_grouped_gemm<true>   gate and up for one (expert, 96-row tile, 32-pair tile):
+//                 A = native MXFP4 weight rows, B = the pairs' x images; epilogue
+//                 bias + activation x routing weight, split into the h images
+//                 [pair][I/32] (the split of k_split_rows).
+//   k_grouped_gemm<false>  down for one (expert, 192-row tile, 32-pair tile) on the
 //                 h images -> o [pair][H].
 //   k_combine     y[t] = sum over t's pairs in ascending expert order of
 //                 (o + w*b_down) (the order of layer.rs:1092-1106).
@@ -123,7 +124,9 @@ struct GroupedArgs {
   const float* pair_w;
   const int32_t* exp_off;
   const int32_t* tile_off;
-  float* out;  // [P][M]
+  float* out;        // [P][M] (down)
+  uint8_t* himg;     // GATEUP: the down input images [P][M/32][kImgBytes]
+  uint32_t* hsc;     // GATEUP: their scale words [P][M/32]
   int M, K, E;
   int act;
   float alpha, limit;
@@ -385,57 +388,102 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) blk[(pg * 16 + i) * kWR + tt * 16 + 4 * g + r] = acc[tt][pg][r];
   __syncthreads();
-  if (GATEUP && m == 0) return;
-  const float* gblk = reinterpret_cast<const float*>(&bst[0][0]) + (wave & 1) * kPairTile * kWR;  // gate
+  if (GATEUP) {
+    // h = act(gate, up) x routing weight, written by the up waves over their gate rows: the
+    // block of gate wave 0 then holds h of tile rows 0-47, gate wave 1's rows 48-95
+    float* gblk = reinterpret_cast<float*>(&bst[0][0]) + (wave & 1) * kPairTile * kWR;
+    if (m == 1) {
+      for (int q = lane; q < np * kWR; q += 64) {
+        const int pl = q / kWR, rr = q - pl * kWR;
+        const int orow = wrow0 + rr;
+        if (orow >= a.M) continue;
+        float gv = gblk[pl * kWR + rr], uv = blk[pl * kWR + rr];
+        if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
+        if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
+        const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
+        gblk[pl * kWR + rr] = h * a.pair_w[p0 + pl];
+      }
+    }
+    __syncthreads();
+    // each (pair, 32-row block) of the tile split into the down input image (the split of
+    // k_split_rows, 8 lanes per block: lane m8 takes elements 2m8, 2m8+16, 2m8+1, 2m8+17)
+    const float* hb = reinterpret_cast<const float*>(&bst[0][0]);
+    const int tr0 = rt * kRows, nbM = a.M >> 5;
+    const int nblk = min(kRows, a.M - tr0) >> 5;  // blocks of this tile (M % 32 == 0)
+    const int m8 = tid & 7;
+    auto hval = [&](int pl, int r) {  // h of tile row r (< 96), pair pl
+      const int half = r >= kWR ? 1 : 0;
+      return hb[(half * kPairTile + pl) * kWR + r - half * kWR];
+    };
+    for (int u = tid >> 3; u < np * nblk; u += kGW * 8) {  // a whole 8-lane group per unit
+      const int pl = u / nblk, b = u - pl * nblk, r0 = 32 * b + 2 * m8;
+      uint32_t codes[kTerms], scales;
+      split_block8(hval(pl, r0), hval(pl, r0 + 16), hval(pl, r0 + 1), hval(pl, r0 + 17), codes, scales);
+      const size_t bi = (size_t)(p0 + pl) * nbM + (tr0 >> 5) + b;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.himg + bi * kImgBytes);
+#pragma unroll
+      for (int t = 0; t < kTerms; ++t) dst[t * 8 + m8] = codes[t];
+      if (m8 == 0) a.hsc[bi] = scales;
+    }
+    return;
+  }
   for (int q = lane; q < np * kWR; q += 64) {
     const int pl = q / kWR, rr = q - pl * kWR;
     const int orow = wrow0 + rr;
     if (orow >= a.M) continue;
-    const int p = p0 + pl;
-    float o = blk[pl * kWR + rr];
-    if (GATEUP) {
-      float gv = gblk[pl * kWR + rr], uv = o;
-      if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
-      if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
-      const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-      o = h * a.pair_w[p];
-    }
-    a.out[(size_t)p * a.M + orow] = o;
+    a.out[(size_t)(p0 + pl) * a.M + orow] = blk[pl * kWR + rr];
   }
 }
 
 // ---- combine -----------------------------------------------------------------------------
 // y[t][row] = sum over t's pairs in ascending pair index (= ascending expert) of
-// o[pair][row] + w * b_down[e][row]. One thread per (token, row); the token's (at most KM)
-// pair indices stay in registers and are taken smallest first.
+// o[pair][row] + w * b_down[e][row]. One thread per (token, 4 rows) on a (row groups, tokens)
+// grid (tokens past gridDim.y loop); the token's (at most KM) pair indices stay in registers and are taken smallest first,
+// and all of a thread's loads issue before the sums. H % 4 == 0.
 template <int KM>
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, const int32_t* __restrict__ pair_of,
                                                  const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                  const float* __restrict__ down_b, int T, int k, int H,
                                                  float* __restrict__ y) {
-  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (long long)T * H) return;
-  const int t = (int)(gid / H), row = (int)(gid % H);
-  int ps[KM];
+  const int row = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (row >= H) return;
+  for (int t = blockIdx.y; t < T; t += gridDim.y) {
+    int ps[KM];
 #pragma unroll
-  for (int s = 0; s < KM; ++s) ps[s] = s < k ? pair_of[t * k + s] : INT_MAX;
-  float acc = 0.f;
+    for (int s = 0; s < KM; ++s) ps[s] = s < k ? pair_of[t * k + s] : INT_MAX;
+    f32x4 v[KM], bv[KM];
+    float wv[KM];
 #pragma unroll
-  for (int r = 0; r < KM; ++r) {
-    if (r < k) {
-      int best = INT_MAX, bs = 0;
+    for (int r = 0; r < KM; ++r) {
+      if (r < k) {
+        int best = INT_MAX, bs = 0;
 #pragma unroll
-      for (int s = 0; s < KM; ++s)
-        if (ps[s] < best) best = ps[s], bs = s;
+        for (int s = 0; s < KM; ++s)
+          if (ps[s] < best) best = ps[s], bs = s;
 #pragma unroll
-      for (int s = 0; s < KM; ++s)
-        if (s == bs) ps[s] = INT_MAX;
-      float v = o[(size_t)best * H + row];
-      if (down_b) v = v + w[t * k + bs] * down_b[(size_t)idx[t * k + bs] * H + row];
-      acc = acc + v;
+        for (int s = 0; s < KM; ++s)
+          if (s == bs) ps[s] = INT_MAX;
+        v[r] = *reinterpret_cast<const f32x4*>(o + (size_t)best * H + row);
+        if (down_b) {
+          wv[r] = w[t * k + bs];
+          bv[r] = *reinterpret_cast<const f32x4*>(down_b + (size_t)idx[t * k + bs] * H + row);
+        }
+      }
     }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+      if (r < k) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float x = v[r][c];
+          if (down_b) x = x + wv[r] * bv[r][c];
+          acc[c] = acc[c] + x;
+        }
+      }
+    }
+    *reinterpret_cast<f32x4*>(y + (size_t)t * H + row) = acc;
   }
-  y[gid] = acc;
 }
 
 // ---- host side -------------------------------------------------------------------------------
@@ -443,7 +491,7 @@ namespace {
 constexpr uint64_t kAlign = 256;
 uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct GroupedPlan {
-  uint64_t pair_tok, pair_w, pair_of, exp_off, tile_off, img_x, sc_x, img_h, sc_h, hbuf, obuf, total;
+  uint64_t pair_tok, pair_w, pair_of, exp_off, tile_off, img_x, sc_x, img_h, sc_h, obuf, total;
 };
 GroupedPlan grouped_plan(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H) {
   GroupedPlan p{};
@@ -458,7 +506,6 @@ GroupedPlan grouped_plan(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.sc_x = o, o += up(T * (H / 32) * 4);
   p.img_h = o, o += up(P * (I / 32) * kImgBytes);
   p.sc_h = o, o += up(P * (I / 32) * 4);
-  p.hbuf = o, o += up(P * I * 4);
   p.obuf = o, o += up(P * H * 4);
   p.total = o;
   return p;
@@ -482,7 +529,6 @@ GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_
   g.sc_x = reinterpret_cast<uint32_t*>(b + p.sc_x);
   g.img_h = reinterpret_cast<uint8_t*>(b + p.img_h);
   g.sc_h = reinterpret_cast<uint32_t*>(b + p.sc_h);
-  g.hbuf = reinterpret_cast<float*>(b + p.hbuf);
   g.obuf = reinterpret_cast<float*>(b + p.obuf);
   return g;
 }
@@ -514,7 +560,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   a.w0 = expert_loc(L.d.gate), a.w1 = expert_loc(L.d.up);
   a.b0 = L.d.gate_bias, a.b1 = L.d.up_bias;
   a.img = gs.img_x, a.isc = gs.sc_x, a.pair_tok = gs.pair_tok, a.pair_w = gs.pair_w;
-  a.exp_off = gs.exp_off, a.tile_off = gs.tile_off, a.out = gs.hbuf;
+  a.exp_off = gs.exp_off, a.tile_off = gs.tile_off, a.himg = gs.img_h, a.hsc = gs.sc_h;
   a.M = I, a.K = H, a.E = E;
   a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   {
@@ -522,13 +568,6 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
     constexpr int rows = (kGW / 2) * kGT * 16;
     hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
                        K.s, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  {
-    ProfScope ps(K, "split_h");
-    const long long nblk = (long long)P * (I / 32);
-    hipLaunchKernelGGL(k_split_rows, dim3((unsigned)((nblk + 31) / 32)), dim3(256), 0, K.s, gs.hbuf, P, I, gs.img_h,
-                       gs.sc_h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   GroupedArgs d{};
@@ -545,8 +584,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   }
   {
     ProfScope ps(K, "combine");
-    const long long n = (long long)T * H;
-    const dim3 grid((unsigned)((n + 255) / 256));
+    const dim3 grid((unsigned)((H / 4 + 255) / 256), std::min<uint32_t>(T, 65535u));
     if (k <= 4)
       hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
                          H, y);

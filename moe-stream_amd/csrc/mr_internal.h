@@ -194,7 +194,6 @@ struct GroupedScratch {
   uint32_t* sc_x;     // [T][H/32]
   uint8_t* img_h;     // [P][I/32][128] h images
   uint32_t* sc_h;     // [P][I/32]
-  float* hbuf;        // [P][I] gate/up results (activation x routing weight)
   float* obuf;        // [P][H] down results
 };
 GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H);
