@@ -128,6 +128,21 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
   v = max(v, dpp_u<kDppMirror>(v));
   return max(max(lane_u<0>(v), lane_u<16>(v)), max(lane_u<32>(v), lane_u<48>(v)));
 }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  auto mx = [](uint64_t a, uint32_t hi, uint32_t lo) {
+    const uint64_t b = ((uint64_t)hi << 32) | lo;
+    return a > b ? a : b;
+  };
+  v = mx(v, dpp_u<kDppXor1>((uint32_t)(v >> 32)), dpp_u<kDppXor1>((uint32_t)v));
+  v = mx(v, dpp_u<kDppXor2>((uint32_t)(v >> 32)), dpp_u<kDppXor2>((uint32_t)v));
+  v = mx(v, dpp_u<kDppHMirror>((uint32_t)(v >> 32)), dpp_u<kDppHMirror>((uint32_t)v));
+  v = mx(v, dpp_u<kDppMirror>((uint32_t)(v >> 32)), dpp_u<kDppMirror>((uint32_t)v));
+  uint64_t r = 0ull;
+  r = mx(r, lane_u<0>((uint32_t)(v >> 32)), lane_u<0>((uint32_t)v));
+  r = mx(r, lane_u<16>((uint32_t)(v >> 32)), lane_u<16>((uint32_t)v));
+  r = mx(r, lane_u<32>((uint32_t)(v >> 32)), lane_u<32>((uint32_t)v));
+  return mx(r, lane_u<48>((uint32_t)(v >> 32)), lane_u<48>((uint32_t)v));
+}
 __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
   v = min(v, dpp_u<kDppXor1>(v));
   v = min(v, dpp_u<kDppXor2>(v));

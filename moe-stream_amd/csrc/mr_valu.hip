@@ -6,6 +6,7 @@
 // MFMA decode kernel (mr_mfma.hip) is checked and timed against, and they run
 // every layout the ABI accepts (MXFP4 and Q4_K, any H, I multiple of the block).
 #include "mr_device.h"
+#include "mr_fused_common.h"
 #include "mr_internal.h"
 
 namespace mr {
@@ -135,16 +136,6 @@ hipError_t launch_router_logits(const Launch& K, const mr_layer& L, const float*
 // fused_ops.metal:131-316). One wave per token; each lane holds up to 8 of the
 // E <= 512 values. Selection = first k of a stable descending sort: the
 // largest value wins, ties go to the lower expert index.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    float ov = __shfl_xor(v, o, kWave);
-    int oi = __shfl_xor(i, o, kWave);
-    bool take = (oi >= 0) && (i < 0 || ov > v || (ov == v && oi < i));
-    if (take) v = ov, i = oi;
-  }
-}
-
 // Top-k of the logits v[j] of experts lane + 64 j (live[j]: e < E).
 __device__ void topk_vals(float (&v)[8], bool (&live)[8], int k, uint32_t flags, int32_t* out_idx,
                           float* out_w, float* sel_v /* LDS [16] */, int* sel_i /* LDS [16] */) {
@@ -170,17 +161,22 @@ __device__ void topk_vals(float (&v)[8], bool (&live)[8], int k, uint32_t flags,
     for (int j = 0; j < 8; ++j)
       if (live[j]) v[j] = v[j] / sum_all;
   }
+  // k rounds of a wave argmax on 64-bit keys: the value's order key above the complemented
+  // expert index, so the larger value wins and, between equal values, the lower index (a NaN
+  // ranks below every number). DPP steps inside 16-lane rows, then the four rows by readlane.
   for (int r = 0; r < k; ++r) {
-    float bv = 0.f;
-    int bi = -1;
+    uint64_t best = 0ull;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      int e = lane + 64 * j;
-      if (live[j] && (bi < 0 || v[j] > bv)) bv = v[j], bi = e;
+      const uint32_t e = (uint32_t)(lane + 64 * j);
+      const uint32_t hk = v[j] == v[j] ? order_key(v[j] + 0.f) : 0u;  // + 0.f: -0.0 ties +0.0
+      const uint64_t key = ((uint64_t)hk << 32) | (0xFFFFFFFFu - e);
+      if (live[j]) best = key > best ? key : best;
     }
-    wave_argmax(bv, bi);
-    if (bi >= 0 && (bi & 63) == lane) live[bi >> 6] = false;
-    if (lane == 0) sel_v[r] = bv, sel_i[r] = bi;
+    best = wave_max_u64(best);
+    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
+    if ((bi & 63) == lane) live[bi >> 6] = false;
+    if (lane == 0) sel_v[r] = key_value((uint32_t)(best >> 32)), sel_i[r] = bi;
   }
   __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
