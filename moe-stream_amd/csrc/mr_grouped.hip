@@ -174,6 +174,8 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bst[kBBuf][kBStep];
   __shared__ __align__(16) uint32_t bsc[kBBuf][kPairTile * 4];
   __shared__ __align__(16) uint8_t ast[kGW][kGT * 16 * kARow];
+  __shared__ float bias_s[GATEUP ? 2 * (kGW / 2) * kGT * 16 + kPairTile : 1];  // GATEUP: the tile's gate,
+                                                                               // up biases, pair weights
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches stay scalar
   const int i = lane & 15, g = lane >> 4;
@@ -205,6 +207,13 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   const uint64_t rb = (uint64_t)nbK * 17;
   const int m = GATEUP ? (wave >> 1) : 0;
   const int wrow0 = rt * kRows + (GATEUP ? (wave & 1) : wave) * (kGT * 16);
+  if (GATEUP && tid < 2 * kRows) {  // read by the epilogue (after the K loop's barriers)
+    const int mat = tid >= kRows, orow = rt * kRows + tid - mat * kRows;
+    const float* bsrc = mat ? a.b1 : a.b0;
+    bias_s[tid] = (bsrc && orow < a.M) ? bsrc[(size_t)e * a.M + orow] : 0.f;
+  }
+  if (GATEUP && tid >= 2 * kRows && tid < 2 * kRows + kPairTile)
+    bias_s[tid] = a.pair_w[p0 + min(tid - 2 * kRows, np - 1)];
   const uint8_t* W = expert_at(m ? a.w1 : a.w0, e);
   bool tin[kGT];  // tile inside the matrix (wave-uniform)
 #pragma unroll
@@ -389,20 +398,18 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
       for (int r = 0; r < 4; ++r) blk[(pg * 16 + i) * kWR + tt * 16 + 4 * g + r] = acc[tt][pg][r];
   __syncthreads();
   if (GATEUP) {
-    // h = act(gate, up) x routing weight, written by the up waves over their gate rows: the
-    // block of gate wave 0 then holds h of tile rows 0-47, gate wave 1's rows 48-95
-    float* gblk = reinterpret_cast<float*>(&bst[0][0]) + (wave & 1) * kPairTile * kWR;
-    if (m == 1) {
-      for (int q = lane; q < np * kWR; q += 64) {
-        const int pl = q / kWR, rr = q - pl * kWR;
-        const int orow = wrow0 + rr;
-        if (orow >= a.M) continue;
-        float gv = gblk[pl * kWR + rr], uv = blk[pl * kWR + rr];
-        if (a.b0) gv = gv + a.b0[(size_t)e * a.M + orow];
-        if (a.b1) uv = uv + a.b1[(size_t)e * a.M + orow];
-        const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-        gblk[pl * kWR + rr] = h * a.pair_w[p0 + pl];
-      }
+    // h = act(gate, up) x routing weight over the gate values, by all four waves: the blocks
+    // of gate waves 0 and 1 then hold h of tile rows 0-47 and 48-95 ([pair][row] each)
+    float* ldsf = reinterpret_cast<float*>(&bst[0][0]);
+    for (int q = tid; q < np * kRows; q += kGW * 64) {
+      const int pl = q / kRows, r = q - pl * kRows;
+      if (rt * kRows + r >= a.M) continue;
+      const int half = r >= kWR ? 1 : 0, at = (half * kPairTile + pl) * kWR + r - half * kWR;
+      float gv = ldsf[at], uv = ldsf[2 * kPairTile * kWR + at];
+      if (a.b0) gv = gv + bias_s[r];
+      if (a.b1) uv = uv + bias_s[kRows + r];
+      const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
+      ldsf[at] = h * bias_s[2 * kRows + pl];
     }
     __syncthreads();
     // each (pair, 32-row block) of the tile split into the down input image (the split of
