@@ -43,41 +43,60 @@ __global__ __launch_bounds__(256) void k_group(const int32_t* __restrict__ idx, 
                                                float* __restrict__ pair_w, int32_t* __restrict__ pair_of,
                                                int32_t* __restrict__ exp_off, int32_t* __restrict__ tile_off) {
   __shared__ int cnt[1024];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   for (int e = tid; e < E; e += 256) cnt[e] = 0;
   __syncthreads();
   constexpr int kGJ = 8;  // entries per thread whose loads are issued together (one round trip)
+  const bool one = P <= 256 * kGJ;  // one pass: the entries and weights stay in registers
+  int ev[kGJ];
+  float wv[kGJ];
   for (int b0 = 0; b0 < P; b0 += 256 * kGJ) {
-    int ev[kGJ];
 #pragma unroll
     for (int j = 0; j < kGJ; ++j) {
       const int q = b0 + 256 * j + tid;
       ev[j] = q < P ? min(max(idx[q], 0), E - 1) : -1;
+      wv[j] = (one && q < P) ? w[q] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < kGJ; ++j)
       if (ev[j] >= 0) atomicAdd(&cnt[ev[j]], 1);
   }
   __syncthreads();
-  if (tid == 0) {  // expert offsets (serial over E <= 1024); cnt becomes the next free position
-    int po = 0, to = 0;
-    for (int e = 0; e < E; ++e) {
-      exp_off[e] = po, tile_off[e] = to;
-      const int c = cnt[e];
-      cnt[e] = po;
-      po += c, to += (c + kPairTile - 1) / kPairTile;
+  if (tid < 64) {  // expert offsets, in expert order: lane l takes experts 16l .. 16l+15 (E <= 1024)
+    int c[16], s = 0, ts = 0;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = 16 * lane + u;
+      c[u] = e < E ? cnt[e] : 0;
+      s += c[u], ts += (c[u] + kPairTile - 1) / kPairTile;
     }
-    exp_off[E] = po, tile_off[E] = to;
+    int po = s, to = ts;  // inclusive prefix over lanes, then exclusive
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(po, o, 64), b = __shfl_up(to, o, 64);
+      if (lane >= o) po += a, to += b;
+    }
+    po -= s, to -= ts;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = 16 * lane + u;
+      if (e < E) {
+        exp_off[e] = po, tile_off[e] = to;
+        cnt[e] = po;  // becomes the next free position
+      }
+      po += c[u], to += (c[u] + kPairTile - 1) / kPairTile;
+    }
+    if (16 * lane < E && E <= 16 * lane + 16) exp_off[E] = po, tile_off[E] = to;
   }
   __syncthreads();
   for (int b0 = 0; b0 < P; b0 += 256 * kGJ) {
-    int ev[kGJ];
-    float wv[kGJ];
+    if (!one) {
 #pragma unroll
-    for (int j = 0; j < kGJ; ++j) {
-      const int q = b0 + 256 * j + tid;
-      ev[j] = q < P ? min(max(idx[q], 0), E - 1) : -1;
-      wv[j] = q < P ? w[q] : 0.f;
+      for (int j = 0; j < kGJ; ++j) {
+        const int q = b0 + 256 * j + tid;
+        ev[j] = q < P ? min(max(idx[q], 0), E - 1) : -1;
+        wv[j] = q < P ? w[q] : 0.f;
+      }
     }
 #pragma unroll
     for (int j = 0; j < kGJ; ++j) {
