@@ -559,6 +559,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
         }
         float r[kQ4DnSlots];
         region_dots<kQ4DnIt, kQ4DnSlots>(ch, qm, nsbI, nsw, xqs, xss, hdec, vbuf, r);
+        XTRACE(wave);  // per wave: dot products and row sums done
 #pragma unroll
         for (int j = 0; j < kQ4DnSlots; ++j)
           if (j < nsw && (lane & 7) == 0) dn_part[wave + 4 * j][lane >> 3] = r[j];
@@ -572,6 +573,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_q4k(Q4Args a) {
           if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
           if (rr < a.H) a.y[rr] = yv;
         }
+        XTRACE(4 + wave);  // per wave: combine done
       }
     }
   }
