@@ -110,24 +110,27 @@ __global__ __launch_bounds__(256) void k_group(const int32_t* __restrict__ idx, 
 }
 
 // ---- activation rows -> B images ------------------------------------------------------------
-// Row r of `src` (D floats) -> img[r][D/32][kImgBytes] + sc[r][D/32]; 8 lanes per block.
+// Row r of `src` (D floats) -> img[r][D/32][kImgBytes] + sc[r][D/32]; 8 lanes per block, on a
+// (block groups of 32, rows) grid (rows past gridDim.y loop).
 __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ src, int n_rows, int D,
                                                     uint8_t* __restrict__ img, uint32_t* __restrict__ sc) {
   const int nb = D >> 5;
-  const long long blk = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int b = blockIdx.x * 32 + (threadIdx.x >> 3);
   const int m = threadIdx.x & 7;
-  const bool in = blk < (long long)n_rows * nb;
-  const long long bb = in ? blk : 0;
-  const float* p = src + (bb / nb) * (long long)D + (bb % nb) * 32 + 2 * m;
-  const f32x2 lo = *reinterpret_cast<const f32x2*>(p);       // elements 2m, 2m+1
-  const f32x2 hi = *reinterpret_cast<const f32x2*>(p + 16);  // elements 2m+16, 2m+17
-  uint32_t codes[kTerms], scales;
-  split_block8(lo.x, hi.x, lo.y, hi.y, codes, scales);
-  if (in) {
-    uint32_t* dst = reinterpret_cast<uint32_t*>(img + bb * kImgBytes);
+  const bool in = b < nb;  // the same for the block's 8 lanes (the split's DPP stays in them)
+  for (int r = blockIdx.y; r < n_rows; r += gridDim.y) {
+    const float* p = src + (size_t)r * D + min(b, nb - 1) * 32 + 2 * m;
+    const f32x2 lo = *reinterpret_cast<const f32x2*>(p);       // elements 2m, 2m+1
+    const f32x2 hi = *reinterpret_cast<const f32x2*>(p + 16);  // elements 2m+16, 2m+17
+    uint32_t codes[kTerms], scales;
+    split_block8(lo.x, hi.x, lo.y, hi.y, codes, scales);
+    if (in) {
+      const size_t bb = (size_t)r * nb + b;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(img + bb * kImgBytes);
 #pragma unroll
-    for (int t = 0; t < kTerms; ++t) dst[t * 8 + m] = codes[t];
-    if (m == 0) sc[bb] = scales;
+      for (int t = 0; t < kTerms; ++t) dst[t * 8 + m] = codes[t];
+      if (m == 0) sc[bb] = scales;
+    }
   }
 }
 
@@ -577,9 +580,8 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   }
   {
     ProfScope ps(K, "split_x");
-    const long long nblk = (long long)T * (H / 32);
-    hipLaunchKernelGGL(k_split_rows, dim3((unsigned)((nblk + 31) / 32)), dim3(256), 0, K.s, x, (int)T, H, gs.img_x,
-                       gs.sc_x);
+    hipLaunchKernelGGL(k_split_rows, dim3((unsigned)((H / 32 + 31) / 32), std::min<uint32_t>(T, 65535u)), dim3(256), 0,
+                       K.s, x, (int)T, H, gs.img_x, gs.sc_x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   GroupedArgs a{};
