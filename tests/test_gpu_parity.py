@@ -251,6 +251,48 @@ def test_grouped_batched_matches_oracle_and_valu(gpu_ctx, layers, T):
         b.free()
 
 
+def test_grouped_batched_many_tokens(gpu_ctx, layers):
+    """600 tokens x top-4 = 2,400 (token, slot) pairs: the grouping kernel's two-pass path
+    (more entries than stay in registers), a ragged last router tile and a long combine grid.
+    Every token against the multi-kernel VALU path; the first and last 8 against the oracle."""
+    if "C5" not in layers:
+        dl = W.DeviceLayer(gpu_ctx, C5_SPEC)
+        host = dict(spec=C5_SPEC)
+        host.update(dl.download_quant())
+        host.update(W.float_tensors(C5_SPEC))
+        layers["C5"] = (dl, host)
+    dl, host = layers["C5"]
+    spec = dl.spec
+    T = 600
+    x = W.x_tokens(spec, T, first_token=1000)
+    dx = gpu_ctx.to_device(x)
+    dy, dv = gpu_ctx.alloc(T * spec.hidden * 4), gpu_ctx.alloc(T * spec.hidden * 4)
+    di, dw, dlg = gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.n_experts * 4)
+    dl.layer.forward_batched(dx, T, dy)
+    dl.layer.router_topk(dx, T, di, dw, dlg)
+    gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_VALU)
+    try:
+        dl.layer.forward_batched(dx, T, dv)
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+    y = dy.download(np.float32).reshape(T, -1)
+    yv = dv.download(np.float32).reshape(T, -1)
+    glg = dlg.download(np.float32).reshape(T, -1)
+    for t in range(T):
+        s = np.sort(glg[t])[::-1]
+        if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(glg[t]).max():
+            assert rel_err(y[t], yv[t]) <= 2 * REL_TOL, (t, rel_err(y[t], yv[t]))
+    sel = np.r_[0:8, T - 8:T]
+    ry, _, _, rlg = oracle.layer_from_host(host).forward(x[sel], n_threads=8)
+    assert np.allclose(glg[sel], rlg, rtol=1e-4, atol=1e-5 * np.abs(rlg).max())
+    for n, t in enumerate(sel):
+        s = np.sort(rlg[n])[::-1]
+        if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg[n]).max():
+            assert rel_err(y[t], ry[n]) <= REL_TOL, (t, rel_err(y[t], ry[n]))
+    for b in (dx, dy, dv, di, dw, dlg):
+        b.free()
+
+
 def test_graph_replay_matches_eager(gpu_ctx, layers):
     dl, _ = get_layer(gpu_ctx, layers, "tiny-q4k-shared")
     spec = dl.spec
