@@ -95,11 +95,15 @@ TINY_Q4 = W.LayerSpec(202, 0, W.GGML_Q4_K, 1024, 512, 16, 4, W.ROUTE_NORM_TOPK, 
 TINY_SH = W.LayerSpec(203, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
                       False, False, sh_inter=256)
 TINY_Q4P = W.LayerSpec(204, 0, W.GGML_Q4_K, 512, 256, 12, 3, 0, W.ACT_SILU, False, False)  # plain softmax
+# top-10 of 20 experts: the 16-slot combine of the grouped path and a ragged 16-expert router tile
+TINY_MXK = W.LayerSpec(205, 0, W.GGML_MXFP4, 512, 384, 20, 10, W.ROUTE_NORM_TOPK, W.ACT_SWIGLU_OAI,
+                       True, True)
 SPECS = {
     "tiny-mxfp4": TINY_MX,
     "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
     "tiny-q4k-shared": TINY_SH,
+    "tiny-mxfp4-k10": TINY_MXK,
     "C1-gpt-oss": W.gpt_oss(1, 0),
     "C3-qwen3-layer0": W.qwen3_30b(3, 0),
     "C4-coder-next-layer0": W.coder_next(4, 0),
@@ -194,7 +198,8 @@ def test_experts_given_routing_parity(gpu_ctx, layers, name):
         b.free()
 
 
-@pytest.mark.parametrize("name,T", [("tiny-mxfp4", 37), ("tiny-q4k-shared", 16), ("C1-gpt-oss", 64)])
+@pytest.mark.parametrize("name,T", [("tiny-mxfp4", 37), ("tiny-q4k-shared", 16), ("tiny-mxfp4-k10", 40),
+                                    ("C1-gpt-oss", 64)])
 def test_batched_parity(gpu_ctx, layers, name, T):
     dl, host = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
