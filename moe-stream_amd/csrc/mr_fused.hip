@@ -466,9 +466,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     const int half = tail >= 0 ? 2 : (q < a.NS ? 1 : 0);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
+    // the routing wave runs at the gate/up waves' priority while it selects (its weight
+    // prefetch, issued after, stays below the gate/up streams)
+    if (wave == 0) __builtin_amdgcn_s_setprio(1);
     if (wave == 0 && !route_select<MR_ROUTE_SLEEP_DOWN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
+    if (wave == 0) __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     TRACE(1);
     if (ok_flag) {
