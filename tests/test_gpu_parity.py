@@ -321,6 +321,35 @@ def test_graph_replay_matches_eager(gpu_ctx, layers):
         b.free()
 
 
+def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
+    """The grouped multi-token path (MFMA router, top-k, grouping, x split, grouped GEMMs with
+    the h split in the epilogue, combine) captured once and replayed: every replay, with eager
+    work in between, gives the eager bits (the grouping's order inside an expert's range varies
+    from run to run; nothing computed depends on it)."""
+    dl, _ = get_layer(gpu_ctx, layers, "tiny-mxfp4-k10")
+    spec = dl.spec
+    T = 40
+    dl.layer.reserve(T)
+    x = W.x_tokens(spec, T, first_token=700)
+    dx = gpu_ctx.to_device(x)
+    dy_e, dy_g = gpu_ctx.alloc(T * spec.hidden * 4), gpu_ctx.alloc(T * spec.hidden * 4)
+    dl.layer.forward_batched(dx, T, dy_e)
+    eager = dy_e.download(np.float32)
+    gpu_ctx.graph_begin()
+    dl.layer.forward_batched(dx, T, dy_g)
+    g = gpu_ctx.graph_end()
+    for rep in range(4):
+        gpu_ctx.check(M.lib.mr_dev_zero(gpu_ctx.h, dy_g.ptr, T * spec.hidden * 4))
+        g.launch()
+        dl.layer.forward_batched(dx, T, dy_e)  # eager work between replays
+        gpu_ctx.sync()
+        assert np.array_equal(dy_g.download(np.float32), eager), rep
+        assert np.array_equal(dy_e.download(np.float32), eager), rep
+    g.close()
+    for b in (dx, dy_e, dy_g):
+        b.free()
+
+
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
