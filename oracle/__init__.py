@@ -113,6 +113,15 @@ def mxfp4_matvec(w: np.ndarray, x: np.ndarray, out_f: int, in_f: int, n_threads:
     return y
 
 
+def mxfp4_matmul(w: np.ndarray, x: np.ndarray, out_f: int, in_f: int, n_threads: int = 1) -> np.ndarray:
+    """x [T, in_f] -> y [T, out_f] (or_mxfp4_matmul, dequant.rs:705-721)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_f)
+    y = np.empty((x.shape[0], out_f), dtype=np.float32)
+    _lib.or_mxfp4_matmul(w.ctypes.data, x.ctypes.data, x.shape[0], out_f, in_f, y.ctypes.data, n_threads)
+    return y
+
+
 def f32_matvec(w: np.ndarray, x: np.ndarray) -> np.ndarray:
     w = np.ascontiguousarray(w, dtype=np.float32)
     x = np.ascontiguousarray(x, dtype=np.float32)

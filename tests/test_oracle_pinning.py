@@ -138,17 +138,81 @@ def test_q4k_mins_only():
         assert np.all(y[sub] == -float(sub + 1)), sub
 
 
+def _pack_q4k_scales(sc, m):
+    """The packing side of the format (ggml's Q4_K quantizer writes the 8 six-bit
+    (scale, min) pairs this way): pairs 0-3 in the low 6 bits of bytes j and j+4; pairs
+    4-7 as nibbles of byte j+4, their high 2 bits in the top bits of bytes j-4 (scale)
+    and j (min). The inverse of get_scale_min_k4, written from the packing rule."""
+    q = np.zeros(12, dtype=np.int64)
+    for j in range(8):
+        if j < 4:
+            q[j] |= sc[j]
+            q[j + 4] |= m[j]
+        else:
+            q[j + 4] = (sc[j] & 0xF) | ((m[j] & 0xF) << 4)
+            q[j - 4] |= (sc[j] >> 4) << 6
+            q[j] |= (m[j] >> 4) << 6
+    return q.astype(np.uint8)
+
+
 @pytest.mark.parametrize("j", range(8))
-def test_get_scale_min_k4_high_bits(j):
-    rng = np.random.default_rng(j)
-    q = rng.integers(0, 256, 12, dtype=np.uint8)
-    sc, m = oracle.get_scale_min_k4(j, q)
-    if j < 4:
-        assert (sc, m) == (q[j] & 63, q[j + 4] & 63)
-    else:
-        assert sc == (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4)
-        assert m == (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
-        assert sc >= 16 * (q[j - 4] >> 6)  # the 2 high bits are really used
+def test_get_scale_min_k4_pack_unpack_round_trip(j):
+    """Every (scale, min) in 0..63 x 0..63 at position j, with random pairs at the other
+    seven positions (so a byte read from the wrong source shows up), packed and unpacked:
+    all eight pairs come back. A swapped high-bit source (q[j-4] vs q[j]) fails here."""
+    rng = np.random.default_rng(100 + j)
+    for s in range(64):
+        for mm in range(64):
+            sc = rng.integers(0, 64, 8)
+            m = rng.integers(0, 64, 8)
+            sc[j], m[j] = s, mm
+            q = _pack_q4k_scales(sc, m)
+            for jj in range(8):
+                assert oracle.get_scale_min_k4(jj, q) == (sc[jj], m[jj]), (j, s, mm, jj)
+
+
+def test_q4k_hand_worked_block_high_bits():
+    """A block worked out by hand with pairs 4-7 above 15 (bits 6-7 of bytes 0-7 set):
+    scales (1, 2, 3, 4, 37, 20, 63, 16), mins (0, 5, 10, 15, 50, 33, 17, 63), d = 1,
+    dmin = 0.5, every quant byte 0x21 (low nibble 1, high nibble 2). Sub-block s takes
+    the low nibbles for even s, high for odd: y_s = sc_s * q - 0.5 * m_s."""
+    scales = np.array([129, 66, 195, 68, 192, 133, 74, 207, 37, 20, 31, 240], dtype=np.uint8)
+    y = oracle.dequant_q4k(_q4k_block(1.0, 0.5, scales, np.full(128, 0x21, np.uint8)), 256).reshape(8, 32)
+    want = [1.0, 1.5, -2.0, 0.5, 12.0, 23.5, 54.5, 0.5]
+    for s in range(8):
+        assert np.all(y[s] == want[s]), (s, y[s][0])
+
+
+# ---- MXFP4 multi-token matmul (dequant.rs:705-721) ----------------------------------------
+
+def test_mxfp4_matmul_one_hot_rows_are_exact_columns():
+    """Token t's input is one-hot at column c_t: row t of the result is column c_t of the
+    dequantized matrix, exactly (pins the [T, in] -> [T, out] layout)."""
+    out_f, in_f = 48, 320
+    w = S.mxfp4_blocks(S.stream_seed(904, 0, 0, 0), out_f * in_f // 32)
+    W_ = npref.mxfp4_dequant(w, out_f * in_f).reshape(out_f, in_f)
+    cols = [0, 17, 31, 32, 200, 319]
+    x = np.zeros((len(cols), in_f), dtype=np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    y = oracle.mxfp4_matmul(w, x, out_f, in_f)
+    for t, c in enumerate(cols):
+        assert np.array_equal(y[t], W_[:, c]), t
+
+
+def test_mxfp4_matmul_f64_bound_and_token_independence():
+    """Random tokens against an f64 product with the dequantized matrix (sequential fp32
+    sums are within in_f * 2^-23 * |W||x|); the result of a token does not depend on the
+    other tokens of the batch (the weights are re-read per token, dequant.rs:705-721)."""
+    out_f, in_f, T = 64, 2880, 5
+    w = S.mxfp4_blocks(S.stream_seed(905, 0, 0, 0), out_f * in_f // 32)
+    x = S.normal(S.stream_seed(905, 1, 0, 0), T * in_f).reshape(T, in_f)
+    W_ = npref.mxfp4_dequant(w, out_f * in_f).reshape(out_f, in_f).astype(np.float64)
+    y = oracle.mxfp4_matmul(w, x, out_f, in_f, 4)
+    ref = x.astype(np.float64) @ W_.T
+    bound = in_f * 2 ** -23 * (np.abs(x.astype(np.float64)) @ np.abs(W_).T)
+    assert np.all(np.abs(y - ref) <= bound)
+    y_rev = oracle.mxfp4_matmul(w, x[::-1].copy(), out_f, in_f, 1)[::-1]
+    assert np.array_equal(y, y_rev)
 
 
 def test_q4k_dequant_matches_numpy_restatement_random():

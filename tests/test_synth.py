@@ -50,7 +50,9 @@ def test_config_shapes_and_bytes():
     # algorithmic bytes per C1 layer-token (MXFP4 weights + biases + router + x/y)
     assert c2[0].weight_bytes_per_token() == 53_406_720 + 128
     c3 = W.config_layers(3)
-    assert sum(s.weight_bytes_per_token() for s in c3) == 48 * (22_298_624 - 0) or True
+    # C3 per layer-token: 8 experts x 3 x 884,736 B + router 128 x 2048 x 4 B + x/y 2 x 8,192 B
+    assert c3[0].weight_bytes_per_token() == 8 * 3 * 884_736 + 1_048_576 + 16_384 == 22_298_624
+    assert sum(s.weight_bytes_per_token() for s in c3) == 48 * 22_298_624 == 1_070_333_952
     c4 = W.config_layers(4)
     assert len(c4) == 48 and all(256 <= s.n_experts <= 512 for s in c4)
     assert len({s.n_experts for s in c4}) > 10
