@@ -44,7 +44,8 @@ def parse():
                     help="do not link each layer to the next (mr_layer_set_next)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=16)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="oracle threads for the CPU baseline (0: every logical core, as the reference's available_parallelism)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel of known size (counter calibration under rocprofv3 --pmc)")
     return ap.parse_args()
@@ -54,32 +55,34 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(layers, specs, n_layers_sample: int, threads: int, budget_s: float = 10.0):
-    """Oracle (C restatement of the reference CPU path) on a bounded sample: the
-    first n_layers_sample layers, one decode token at a time, until about
-    budget_s seconds of CPU work. Returns (layer-tokens/s, layer-tokens timed)."""
+def cpu_baseline(layers, specs, threads: int, budget_s: float = 12.0):
+    """The oracle (C restatement of the reference CPU path) on a bounded sample of the
+    workload: the same N decode tokens through every layer of the stack, one layer's
+    weights on the host at a time, with N sized from a one-token calibration on the first
+    layer so that the sample takes about budget_s of CPU work. A token's time is the sum
+    of its layers' times, so tokens/s = N / (total time). Returns (tokens/s, N, seconds)."""
     import oracle  # test infrastructure; used here only as the timed CPU baseline
     from moe_rocm import workloads as W
 
-    per_layer = budget_s / n_layers_sample
-    t_total, n_lt = 0.0, 0
-    for li in range(n_layers_sample):
-        dl, spec = layers[li], specs[li]
+    n_tok, total = None, 0.0
+    for dl, spec in zip(layers, specs):
         host = dict(spec=spec)
         host.update(dl.download_quant())
         host.update(W.float_tensors(spec))
         L = oracle.layer_from_host(host)
-        x = W.x_tokens(spec, 1024)
-        L.forward(x[:1], n_threads=threads)  # warm-up
+        if n_tok is None:
+            x1 = W.x_tokens(spec, 1)
+            L.forward(x1, n_threads=threads)  # warm-up
+            t0 = time.perf_counter()
+            L.forward(x1, n_threads=threads)
+            n_tok = max(1, int(budget_s / (len(specs) * (time.perf_counter() - t0))))
+        x = W.x_tokens(spec, n_tok)
         t0 = time.perf_counter()
-        t = 0
-        while t < len(x) and time.perf_counter() - t0 < per_layer:
+        for t in range(n_tok):
             L.forward(x[t:t + 1], n_threads=threads)
-            t += 1
-        t_total += time.perf_counter() - t0
-        n_lt += t
+        total += time.perf_counter() - t0
         del host, L
-    return n_lt / t_total, n_lt
+    return n_tok / total, n_tok, total
 
 
 def copy_calibration(n_bytes: int = 1 << 30, reps: int = 4) -> None:
@@ -105,6 +108,64 @@ def measured_traffic(config: int):
     if not f.exists():
         return None
     return json.loads(f.read_text()).get(f"C{config}")
+
+
+def host_cpu() -> dict:
+    """Logical core count and model name of this host (/proc/cpuinfo)."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"logical_cores": os.cpu_count(), "model": model}
+
+
+def output_check(ctx, M, W, stack, y, t_last: int, kernel_opt: int) -> dict:
+    """After the timed region: every layer's output of the last timed token, as the token
+    graphs left it, against an eager run of the same layer and input through the
+    multi-kernel VALU path (another kernel family; each is within 1e-3 of the oracle, so
+    the two agree within 2e-3). A layer whose router logits (recomputed in float64 on the
+    host) put the k-th and (k+1)-th expert within 1e-5 of the largest logit may route
+    differently on the two paths and is reported as tie-ambiguous instead of compared."""
+    H = stack.H
+    tmp = ctx.alloc(H * 4)
+    x_all = stack.d_x.download(np.float32, count=stack.n_layers * H,
+                               offset=t_last * stack.n_layers * H * 4).reshape(stack.n_layers, H)
+    worst, compared, ambiguous = 0.0, 0, []
+    prev = None
+    try:
+        ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_VALU)
+        for li, dl in enumerate(stack.layers):
+            spec = dl.spec
+            xp = stack.x_ptr(t_last, li)
+            x = x_all[li].astype(np.float64)
+            if stack.residual:
+                dl.layer.forward_residual(xp, stack.d_nw.ptr + li * H * 4, stack.eps, tmp)
+                xin = x / np.sqrt((x * x).mean() + stack.eps) * stack.norm_w[li]
+            else:
+                dl.layer.forward(xp, tmp)
+                xin = x
+            ref = tmp.download(np.float32).astype(np.float64)
+            rw = dl.f["router_w"].download(np.float32).reshape(spec.n_experts, H).astype(np.float64)
+            lg = rw @ xin
+            if dl.f["router_b"] is not None:
+                lg += dl.f["router_b"].download(np.float32)
+            s = np.sort(lg)[::-1]
+            if s[spec.top_k - 1] - s[spec.top_k] <= 1e-5 * np.abs(lg).max():
+                ambiguous.append(li)
+                continue
+            moe = ref - x if stack.residual else ref
+            err = float(np.abs(y[li] - ref).max() / max(np.abs(moe).max(), 1e-30))
+            worst = max(worst, err)
+            compared += 1
+    finally:
+        ctx.set_option(M.OPT_DECODE_KERNEL, kernel_opt)
+        tmp.free()
+    return {"token": t_last, "layers_compared": compared, "tie_ambiguous_layers": ambiguous,
+            "max_rel_err_vs_valu": worst, "tolerance": 2e-3, "pass": bool(compared > 0 and worst <= 2e-3)}
 
 
 MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 (the f8f6f4 MFMA with an fp8 B operand)
@@ -173,7 +234,7 @@ def bench_batched(a, ctx, M, W, spec):
         host.update(dl.download_quant())
         host.update(W.float_tensors(spec))
         L = oracle.layer_from_host(host)
-        threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
+        threads = a.cpu_threads or os.cpu_count() or 1
         L.forward(x[:1], n_threads=threads)
         t0 = time.perf_counter()
         ns = 0
@@ -182,13 +243,14 @@ def bench_batched(a, ctx, M, W, spec):
             ns += 8
         dt = time.perf_counter() - t0
         cpu = {"value": round(ns / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "host": host_cpu(),
                "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on {ns} of the "
                          f"{T} tokens"}
     out = {
         "metric": "expert-FFN batched/prefill tokens/s + MFMA utilisation, GPT-OSS-20B shape",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(ms / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "mxfp4-weights/e4m3x4-activations/f32-acc",
+        "dtype": "mxfp4-weights/e4m3x4-act/f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1); Zipf(1.1) router skew)",
         "config": {"workload": W.CONFIG_NAMES[5], "config_id": 5, "tokens": T, "hidden": H, "inter": I,
                    "experts": spec.n_experts, "top_k": spec.top_k, "graph": g is not None},
@@ -219,8 +281,8 @@ def main():
     from moe_rocm import workloads as W
 
     ctx = M.Context(0)
-    if a.kernel != "auto":
-        ctx.set_option(M.OPT_DECODE_KERNEL, {"valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel])
+    kernel_opt = {"auto": M.DECODE_AUTO, "valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel]
+    ctx.set_option(M.OPT_DECODE_KERNEL, kernel_opt)
     specs = W.config_layers(a.config)
     if a.config == 5:
         bench_batched(a, ctx, M, W, specs[0])
@@ -229,65 +291,34 @@ def main():
     K, Wm = a.steps, a.warmup
     n_tok = K + Wm
     t0 = time.perf_counter()
-    layers = [W.DeviceLayer(ctx, s) for s in specs]
-    for dl in layers:
-        dl.layer.reserve(1)
-    if not a.no_prefetch_hint:  # decode order: layer l, then l+1; the last, then the next token's first
-        for li, dl in enumerate(layers):
-            dl.layer.set_next(layers[(li + 1) % n_layers].layer)
+    stack = W.DecodeStack(ctx, specs, residual=a.residual, prefetch_hint=not a.no_prefetch_hint)
+    layers = stack.layers
     log(f"built {n_layers} layers in {time.perf_counter() - t0:.1f}s")
-    H = specs[0].hidden
     # inputs: x[token][layer] resident in HBM before the timed region
-    xs = np.empty((n_tok, n_layers, H), dtype=np.float32)
-    for li, s in enumerate(specs):
-        xs[:, li, :] = W.x_tokens(s, n_tok)
-    d_x = ctx.to_device(xs)
-    d_y = ctx.zeros((n_layers, H))
-    ctx.sync()
-    xb, yb = d_x.ptr, d_y.ptr
-
-    if a.residual:  # synthetic post-attention norm weights, one vector per layer
-        rng = np.random.default_rng(20261201)
-        d_nw = ctx.to_device((1.0 + 0.1 * rng.standard_normal((n_layers, H))).astype(np.float32))
-
-    def enqueue_token(t):
-        for li, dl in enumerate(layers):
-            if a.residual:
-                dl.layer.forward_residual(xb + ((t * n_layers + li) * H) * 4, d_nw.ptr + li * H * 4, 1e-5,
-                                          yb + li * H * 4)
-            else:
-                dl.layer.forward(xb + ((t * n_layers + li) * H) * 4, yb + li * H * 4)
-
-    graphs = []
+    stack.load(stack.inputs(n_tok))
     if not a.no_graph:
         t0 = time.perf_counter()
-        for t in range(n_tok):
-            ctx.graph_begin()
-            enqueue_token(t)
-            graphs.append(ctx.graph_end())
-        log(f"captured {len(graphs)} token graphs in {time.perf_counter() - t0:.1f}s")
-
-    def run(t):
-        if graphs:
-            graphs[t].launch()
-        else:
-            enqueue_token(t)
+        stack.capture()
+        log(f"captured {len(stack.graphs)} token graphs in {time.perf_counter() - t0:.1f}s")
 
     for t in range(Wm):
-        run(t)
+        stack.run(t)
     ctx.sync()
     wall0 = time.perf_counter()
     ctx.timer_start()
     for t in range(Wm, n_tok):
-        run(t)
+        stack.run(t)
     ms = ctx.timer_stop()
     wall = time.perf_counter() - wall0
+    ctx.sync()  # also reports a fused launch whose cross-workgroup wait ran out
     tok_s = K / (ms / 1e3)
     if a.config == 1:  # unit: one token through one layer (the 8 instances are independent copies)
         tok_s = K * n_layers / (ms / 1e3)
-    y = d_y.download(np.float32)
+    y = stack.outputs()
     assert np.all(np.isfinite(y)), "non-finite output"
     log(f"timed {K} tokens: {ms:.2f} ms (event), {wall * 1e3:.2f} ms (wall) -> {tok_s:.1f} tok/s")
+    check = output_check(ctx, M, W, stack, y, n_tok - 1, kernel_opt)
+    log(f"output check: {check}")
 
     bytes_per_token = sum(s.weight_bytes_per_token() for s in specs)
     flops_per_token = sum(s.flops_per_token() for s in specs)
@@ -297,7 +328,7 @@ def main():
     ctx.profile_reset()
     P = min(a.profile_tokens, n_tok)
     for t in range(P):
-        enqueue_token(t)
+        stack.enqueue_token(t)
     ctx.sync()
     kern = {}
     for name in ("fused_layer", "gateup", "down", "router_logits", "topk", "shared_gateup"):
@@ -333,16 +364,17 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        threads = max(1, min(a.cpu_threads, os.cpu_count() or 1))
-        nls = min(2, n_layers)
+        threads = a.cpu_threads or os.cpu_count() or 1
         t0 = time.perf_counter()
-        lt_s, n_lt = cpu_baseline(layers, specs, nls, threads)
-        log(f"cpu baseline: {lt_s:.1f} layer-tok/s ({n_lt} layer-tokens) in {time.perf_counter() - t0:.1f}s")
-        cpu = {"value": round(lt_s if a.config == 1 else lt_s / n_layers, 3), "unit": unit, "cores": threads,
-               "kind": "port",
-               "sample": f"oracle (C restatement of the reference CPU path, {threads} threads), one decode token "
-                         f"at a time, on {nls} of the {n_layers} layers for ~10 s ({n_lt} layer-tokens); "
-                         + (f"tokens/s = layer-tokens/s / {n_layers}" if a.config != 1 else "layer-tokens/s")}
+        tok_cpu, n_cpu, sec = cpu_baseline(layers, specs, threads)
+        log(f"cpu baseline: {tok_cpu:.3f} tok/s ({n_cpu} tokens x {n_layers} layers, {sec:.1f}s of oracle time) "
+            f"in {time.perf_counter() - t0:.1f}s")
+        cpu = {"value": round(tok_cpu * n_layers if a.config == 1 else tok_cpu, 3), "unit": unit, "cores": threads,
+               "host": host_cpu(), "kind": "port",
+               "sample": f"oracle (C restatement of the reference CPU path; MXFP4 matvec rows and F32 GEMV rows "
+                         f"split over {threads} threads, Q4_K dequant single-threaded as in the reference): the same "
+                         f"{n_cpu} decode tokens through each of the {n_layers} layers, one layer resident on the host "
+                         f"at a time, {sec:.1f} s of CPU work"}
 
     out = {
         "metric": "expert-FFN decode tokens/s + achieved HBM GB/s (% peak), GPT-OSS-20B shape",
@@ -355,7 +387,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4-weights/f32" if s0.mxfp4 else "q4_k-weights/f32",
+        # what the kernels compute: MXFP4 weights on the scaled MFMA against the activation
+        # split into 4 e4m3 terms per 32-element block; Q4_K weights on int8 dot products
+        # against the activation split into 2 int8 terms per 16-element group; f32 accumulation
+        "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if s0.mxfp4 else "q4_k-weights/int8x2-act/f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1))",
         "config": {"workload": W.CONFIG_NAMES[a.config], "config_id": a.config,
                    "layers": n_layers, "tokens": K, "hidden": s0.hidden, "inter": s0.inter,
@@ -372,13 +407,14 @@ def main():
                      "avg_launch_us": round(avg_ms * 1e3, 3), "avg_launch_method": avg_how,
                      "traffic_source": None if traffic is None else "profiles/traffic.json (rocprofv3 --pmc)"},
         "cpu_baseline": cpu,
+        "output_check": check,
     }
     print(json.dumps(out), flush=True)
-    for g in graphs:
-        g.close()
-    for dl in layers:
-        dl.close()
+    stack.close()
     ctx.close()
+    if not check["pass"]:
+        log("output check FAILED: the timed pipeline's outputs disagree with the eager VALU path")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -266,3 +266,99 @@ class DeviceLayer:
             if b is not None:
                 b.free()
 
+
+
+def norm_weights(n_layers: int, hidden: int) -> np.ndarray:
+    """Synthetic post-attention RMSNorm weights, one vector per layer: 1 + 0.1 N(0,1)."""
+    rng = np.random.default_rng(20261201)
+    return (1.0 + 0.1 * rng.standard_normal((n_layers, hidden))).astype(np.float32)
+
+
+class DecodeStack:
+    """The batch-1 decode pipeline the benchmark times: the layers of a stack on the GPU,
+    each linked to the one that runs after it (mr_layer_set_next; the last layer to the
+    first, where the next token starts), the inputs x[token][layer] resident in HBM, and
+    one HIP graph per token holding that token's layer launches in order. Layer l of
+    token t reads x[t][l] and writes y[l] (mr_moe_forward), or with residual=True writes
+    y[l] = x[t][l] + moe(rms_norm(x[t][l])) (mr_moe_forward_residual)."""
+
+    def __init__(self, ctx, specs, *, residual: bool = False, prefetch_hint: bool = True):
+        self.ctx, self.specs, self.residual = ctx, list(specs), residual
+        self.layers = [DeviceLayer(ctx, s) for s in self.specs]
+        for dl in self.layers:
+            dl.layer.reserve(1)
+        n = len(self.layers)
+        if prefetch_hint:
+            for li, dl in enumerate(self.layers):
+                dl.layer.set_next(self.layers[(li + 1) % n].layer)
+        self.H = self.specs[0].hidden
+        self.eps = 1e-5
+        self.norm_w = norm_weights(n, self.H) if residual else None
+        self.d_nw = ctx.to_device(self.norm_w) if residual else None
+        self.d_x = self.d_y = None
+        self.graphs: list = []
+
+    @property
+    def n_layers(self) -> int:
+        return len(self.layers)
+
+    def inputs(self, n_tokens: int, first_token: int = 0) -> np.ndarray:
+        """x[token][layer] ~ N(0,1), one stream per (layer, token)."""
+        xs = np.empty((n_tokens, self.n_layers, self.H), dtype=np.float32)
+        for li, s in enumerate(self.specs):
+            xs[:, li, :] = x_tokens(s, n_tokens, first_token)
+        return xs
+
+    def load(self, xs: np.ndarray) -> None:
+        """Uploads the inputs and clears the outputs y[layer]."""
+        for b in (self.d_x, self.d_y):
+            if b is not None:
+                b.free()
+        self.n_tokens = xs.shape[0]
+        self.d_x = self.ctx.to_device(np.ascontiguousarray(xs, dtype=np.float32))
+        self.d_y = self.ctx.zeros((self.n_layers, self.H))
+        self.ctx.sync()
+
+    def x_ptr(self, t: int, li: int) -> int:
+        return self.d_x.ptr + ((t * self.n_layers + li) * self.H) * 4
+
+    def y_ptr(self, li: int) -> int:
+        return self.d_y.ptr + li * self.H * 4
+
+    def enqueue_token(self, t: int) -> None:
+        for li, dl in enumerate(self.layers):
+            if self.residual:
+                dl.layer.forward_residual(self.x_ptr(t, li), self.d_nw.ptr + li * self.H * 4, self.eps,
+                                          self.y_ptr(li))
+            else:
+                dl.layer.forward(self.x_ptr(t, li), self.y_ptr(li))
+
+    def capture(self) -> None:
+        """One graph per loaded token."""
+        self.close_graphs()
+        for t in range(self.n_tokens):
+            self.ctx.graph_begin()
+            self.enqueue_token(t)
+            self.graphs.append(self.ctx.graph_end())
+
+    def run(self, t: int) -> None:
+        if self.graphs:
+            self.graphs[t].launch()
+        else:
+            self.enqueue_token(t)
+
+    def outputs(self) -> np.ndarray:
+        return self.d_y.download(np.float32).reshape(self.n_layers, self.H)
+
+    def close_graphs(self) -> None:
+        for g in self.graphs:
+            g.close()
+        self.graphs = []
+
+    def close(self) -> None:
+        self.close_graphs()
+        for b in (self.d_x, self.d_y, self.d_nw):
+            if b is not None:
+                b.free()
+        for dl in self.layers:
+            dl.close()

@@ -204,6 +204,48 @@ void or_f32_matvec(const float* w, const float* x, size_t out_features, size_t i
   }
 }
 
+/* or_f32_matvec with its rows split over threads (candle's F32 matmul runs on a thread
+ * pool); each row is the same sequential sum, so the bits do not depend on the split. */
+typedef struct {
+  const float *w, *x;
+  float* y;
+  size_t r0, r1, in_features;
+} f32_job;
+
+static void* f32_rows_thread(void* p) {
+  const f32_job* jb = (const f32_job*)p;
+  or_f32_matvec(jb->w + jb->r0 * jb->in_features, jb->x, jb->r1 - jb->r0, jb->in_features, jb->y + jb->r0);
+  return NULL;
+}
+
+static void f32_matvec_mt(const float* w, const float* x, size_t out_features, size_t in_features, float* y,
+                          int n_threads) {
+  size_t nt = n_threads < 1 ? 1 : (size_t)n_threads;
+  if (nt > 256) nt = 256;
+  if (nt > out_features) nt = out_features;
+  if (nt <= 1) {
+    or_f32_matvec(w, x, out_features, in_features, y);
+    return;
+  }
+  size_t chunk = (out_features + nt - 1) / nt;
+  pthread_t tid[256];
+  f32_job jobs[256];
+  size_t launched = 0;
+  for (size_t c = 0; c < nt; ++c) {
+    size_t r0 = c * chunk, r1 = r0 + chunk;
+    if (r0 >= out_features) break;
+    if (r1 > out_features) r1 = out_features;
+    jobs[c] = (f32_job){w, x, y, r0, r1, in_features};
+    if (pthread_create(&tid[c], NULL, f32_rows_thread, &jobs[c]) != 0) {
+      f32_rows_thread(&jobs[c]);
+      tid[c] = 0;
+    }
+    launched = c + 1;
+  }
+  for (size_t c = 0; c < launched; ++c)
+    if (tid[c]) pthread_join(tid[c], NULL);
+}
+
 /* ---- routing: layer.rs:2346-2403 top_k_routing ---------------------------- */
 
 /* First k entries of a stable descending sort (Rust sort_by with
@@ -322,8 +364,8 @@ static void expert_matvec(int type, const uint8_t* wq, size_t rows, size_t cols,
   if (type == OR_GGML_MXFP4) {
     or_mxfp4_matvec(wq, in, rows, cols, out, n_threads);
   } else {
-    or_dequant_q4k(wq, rows * cols, deq_scratch);
-    or_f32_matvec(deq_scratch, in, rows, cols, out);
+    or_dequant_q4k(wq, rows * cols, deq_scratch);  /* single-threaded, as dequant.rs:218 */
+    f32_matvec_mt(deq_scratch, in, rows, cols, out, n_threads);
   }
 }
 
@@ -346,7 +388,7 @@ static void expert_ffn(const or_layer* L, uint32_t e, const float* x, float* o, 
     for (size_t j = 0; j < H; ++j) o[j] = o[j] + L->down_b[(size_t)e * H + j];
 }
 
-static int shared_expert(const or_layer* L, const float* x, float* y);
+static int shared_expert(const or_layer* L, const float* x, float* y, int n_threads);
 
 /* Expert assignment (layer.rs:1092-1106): experts visited in ascending index
  * order; each assigned token gets y[t] += out * w (layer.rs:1446-1448,
@@ -380,13 +422,13 @@ int or_moe_experts(const or_layer* L, const float* x, size_t n_tokens, const uin
   free(o), free(g), free(u), free(deq);
   int rc = 0;
   if (L->sh_gate)
-    for (size_t t = 0; t < n_tokens && rc == 0; ++t) rc = shared_expert(L, x + t * H, y + t * H);
+    for (size_t t = 0; t < n_tokens && rc == 0; ++t) rc = shared_expert(L, x + t * H, y + t * H, n_threads);
   return rc;
 }
 
 /* Shared expert (layer.rs:1898-1953): dense SwiGLU on dequantized F32 weights,
  * scaled by sigmoid(sum(x * gate_inp)), added after the routed sum. */
-static int shared_expert(const or_layer* L, const float* x, float* y) {
+static int shared_expert(const or_layer* L, const float* x, float* y, int n_threads) {
   size_t H = L->hidden, I = L->sh_inter;
   float* deq = (float*)malloc(sizeof(float) * H * I);
   float* g = (float*)malloc(sizeof(float) * I);
@@ -396,10 +438,10 @@ static int shared_expert(const or_layer* L, const float* x, float* y) {
     free(deq), free(g), free(u), free(s);
     return -1;
   }
-  expert_matvec(L->sh_type, L->sh_gate, I, H, x, g, deq, 1);
-  expert_matvec(L->sh_type, L->sh_up, I, H, x, u, deq, 1);
+  expert_matvec(L->sh_type, L->sh_gate, I, H, x, g, deq, n_threads);
+  expert_matvec(L->sh_type, L->sh_up, I, H, x, u, deq, n_threads);
   for (size_t i = 0; i < I; ++i) g[i] = or_silu_mul1(g[i], u[i]);
-  expert_matvec(L->sh_type, L->sh_down, H, I, g, s, deq, 1);
+  expert_matvec(L->sh_type, L->sh_down, H, I, g, s, deq, n_threads);
   if (L->sh_gate_inp) {
     float z = 0.0f;
     for (size_t j = 0; j < H; ++j) z = z + x[j] * L->sh_gate_inp[j];

@@ -108,6 +108,9 @@ SPECS = {
     "C3-qwen3-layer0": W.qwen3_30b(3, 0),
     "C4-coder-next-layer0": W.coder_next(4, 0),
 }
+# C4 layers across the range of expert counts: 260 (layer 14), 454 (layer 2) and 510 (layer 26).
+# Above 448 experts all eight per-lane key columns of the fused routing are live.
+C4_RANGE = {f"C4-coder-next-layer{l}-E{W.coder_next(4, l).n_experts}": W.coder_next(4, l) for l in (14, 2, 26)}
 
 
 @pytest.fixture(scope="module")
@@ -120,7 +123,7 @@ def layers(gpu_ctx):
 
 def get_layer(gpu_ctx, layers, name):
     if name not in layers:
-        spec = SPECS[name]
+        spec = SPECS[name] if name in SPECS else C4_RANGE[name]
         dl = W.DeviceLayer(gpu_ctx, spec)
         host = dict(spec=spec)
         host.update(dl.download_quant())
@@ -353,7 +356,7 @@ def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
-         "C4-coder-next-layer0"]
+         "C4-coder-next-layer0", *C4_RANGE]
 
 
 @pytest.mark.parametrize("name", FUSED)
@@ -583,6 +586,11 @@ TIE_SPECS = {
                               W.ACT_SWIGLU_OAI, True, True),
     "q4k-E300": W.LayerSpec(211, 0, W.GGML_Q4_K, 256, 256, 300, 10, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, True),
     "q4k-E100": W.LayerSpec(212, 0, W.GGML_Q4_K, 256, 256, 100, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, True),
+    # 512 experts: every per-lane key column live; all-equal and tied-top put more than 64 keys at or
+    # above the k-th largest lane maximum, so the selection searches all columns
+    "q4k-E512": W.LayerSpec(213, 0, W.GGML_Q4_K, 256, 256, 512, 10, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, True),
+    "q4k-E512-shared": W.LayerSpec(214, 0, W.GGML_Q4_K, 256, 256, 512, 10, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
+                                   True, sh_inter=256),
 }
 
 

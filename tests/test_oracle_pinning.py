@@ -370,3 +370,14 @@ def test_rms_norm_invariants():
     assert np.allclose((u.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-6)
     # eps enters under the root: a large eps shrinks the output
     assert np.all(np.abs(oracle.rms_norm(x, w, 100.0)) < np.abs(a) + 1e-7)
+
+
+@pytest.mark.parametrize("spec", [TINY_Q4, TINY_SH], ids=["q4k", "q4k+shared"])
+def test_q4k_layer_thread_split_is_bit_identical(spec):
+    """The F32 GEMV rows of the Q4_K path are split over threads; every row keeps its
+    sequential sum, so any thread count gives the same bits."""
+    L = oracle.layer_from_host(W.host_layer(spec))
+    x = W.x_tokens(spec, 2)
+    y1 = L.forward(x, n_threads=1)[0]
+    for nt in (3, 8):
+        assert np.array_equal(L.forward(x, n_threads=nt)[0].view(np.uint32), y1.view(np.uint32)), nt
