@@ -141,17 +141,14 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   uint64_t nE = std::max<uint64_t>(E, s.cap_e), nI = std::max<uint64_t>(I, s.cap_i);
   uint64_t nH = std::max<uint64_t>(H, s.cap_h), nS = std::max<uint64_t>(Ish, s.cap_ish);
   ScratchPlan p = plan_scratch(nT, nk, nE, nI, nH, nS);
-  if (s.base) {
-    hipError_t e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
-    (void)hipFree(s.base);
-    s.base = nullptr;
-  }
   void* base = nullptr;
   hipError_t e = hipMalloc(&base, p.total);
-  if (e != hipSuccess) {
-    s = mr::Scratch{};
-    return hip_fail(c, e, "hipMalloc(scratch)");
+  if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
+  if (s.base) {
+    // a graph captured before may still address the old allocation: keep it
+    c->retired.push_back(s.base);
+    c->retired_err.push_back(s.sync + mr::kSyncErrWord);
+    s.base = nullptr;
   }
   // sync words and counters must start at zero; later calls keep them balanced
   e = mr::launch_zero(mr::Launch{c->stream, nullptr}, base, p.total);
@@ -172,6 +169,18 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   s.xn = reinterpret_cast<float*>(b + p.xn);
   s.ytmp = reinterpret_cast<float*>(b + p.ytmp);
   s.cap_tokens = nT, s.cap_k = nk, s.cap_e = nE, s.cap_i = nI, s.cap_h = nH, s.cap_ish = nS;
+  return MR_OK;
+}
+
+bool misaligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; }
+
+// Kernels read f32 activations and router rows as 16-byte vectors and index/weight
+// arrays as 4-byte words.
+int check_io_align(mr_ctx* c, const float* x, const float* y, const void* idx, const float* w, const float* logits) {
+  if (misaligned(x, 16) || misaligned(y, 16))
+    return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
+  if (misaligned(idx, 4) || misaligned(w, 4) || misaligned(logits, 4))
+    return set_err(c, MR_E_INVAL, "idx, w and logits must be 4-byte aligned");
   return MR_OK;
 }
 
@@ -261,6 +270,7 @@ void mr_ctx_destroy(mr_ctx* c) {
     (void)bind(c);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch.base) (void)hipFree(c->scratch.base);
+    for (void* r : c->retired) (void)hipFree(r);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     for (hipEvent_t ev : c->prof.pool) (void)hipEventDestroy(ev);
@@ -315,16 +325,24 @@ int mr_sync(mr_ctx* c) {
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
   if (c->fused_used && c->scratch.sync) {
-    uint32_t word = 0;
-    uint32_t* dev = c->scratch.sync + mr::kSyncErrWord;
-    e = hipMemcpy(&word, dev, 4, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(c, e, "read fused error word");
-    if (word) {
-      const uint32_t zero = 0;
-      e = hipMemcpy(dev, &zero, 4, hipMemcpyHostToDevice);
-      if (e != hipSuccess) return hip_fail(c, e, "reset fused error word");
-      return set_err(c, MR_E_LAUNCH, "fused decode kernel: a cross-workgroup wait ran out (results of that launch are invalid)");
+    // the current scratch's error word and those of superseded scratch (graphs captured
+    // before the scratch grew still write there)
+    bool ran_out = false;
+    const size_t n_words = 1 + c->retired_err.size();
+    for (size_t i = 0; i < n_words; ++i) {
+      uint32_t* dev = i == 0 ? c->scratch.sync + mr::kSyncErrWord : c->retired_err[i - 1];
+      uint32_t word = 0;
+      e = hipMemcpy(&word, dev, 4, hipMemcpyDeviceToHost);
+      if (e != hipSuccess) return hip_fail(c, e, "read fused error word");
+      if (word) {
+        const uint32_t zero = 0;
+        e = hipMemcpy(dev, &zero, 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(c, e, "reset fused error word");
+        ran_out = true;
+      }
     }
+    if (ran_out)
+      return set_err(c, MR_E_LAUNCH, "fused decode kernel: a cross-workgroup wait ran out (results of that launch are invalid)");
   }
   return MR_OK;
 }
@@ -491,6 +509,10 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   if (d->down->out_features != H || d->down->in_features != I)
     return set_err(c, MR_E_INVAL, "down pack is [%u,%u], expected [%u,%u]", d->down->out_features, d->down->in_features, H, I);
   if (!d->router_w) return set_err(c, MR_E_INVAL, "router weights are required");
+  for (const float* f : {d->router_w, d->router_b, d->dummy_mask, d->gate_bias, d->up_bias, d->down_bias,
+                         d->sh_gate_inp})
+    if (misaligned(f, 16))
+      return set_err(c, MR_E_INVAL, "router, bias, mask and shared-gate arrays must be 16-byte aligned");
   if (E > mr::kMaxExperts) return set_err(c, MR_E_UNSUPPORTED, "n_experts %u > %u", E, mr::kMaxExperts);
   if (d->top_k == 0 || d->top_k > mr::kMaxTopK || d->top_k > E)
     return set_err(c, MR_E_INVAL, "top_k %u must be in 1..min(16, E=%u)", d->top_k, E);
@@ -522,7 +544,8 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   L->ctx = c;
   L->d = *d;
   L->H = H, L->I = I, L->E = E, L->Ish = Ish, L->type = type;
-  if (has_dev(c) && (mr::fused_supported(*L, c->n_cu) || mr::fused_q4k_supported(*L, c->n_cu))) {
+  if (has_dev(c) && ((mr::fused_supported(*L, c->n_cu) && mr::fused_resident(*L, c->n_cu)) ||
+                     (mr::fused_q4k_supported(*L, c->n_cu) && mr::fused_q4k_resident(*L, c->n_cu)))) {
     // sync block of the fused decode kernel: counters start at zero
     int rc = bind(c);
     void* fs = nullptr;
@@ -575,6 +598,7 @@ int mr_router_topk(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, int
   int rc = check_layer(c, L);
   if (rc) return rc;
   if (!x || !idx || !w) return set_err(c, MR_E_INVAL, "NULL x, idx or w");
+  if ((rc = check_io_align(c, x, nullptr, idx, w, logits))) return rc;
   if (T == 0) return MR_OK;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
@@ -590,10 +614,11 @@ int mr_topk(mr_ctx* c, const float* logits, uint32_t T, uint32_t E, uint32_t k, 
   if (E == 0 || E > mr::kMaxExperts) return set_err(c, MR_E_INVAL, "n_experts %u must be in 1..%u", E, mr::kMaxExperts);
   if (k == 0 || k > mr::kMaxTopK || k > E) return set_err(c, MR_E_INVAL, "top_k %u must be in 1..min(16, %u)", k, E);
   if (flags & ~(MR_ROUTE_SOFTMAX_AFTER_TOPK | MR_ROUTE_NORM_TOPK)) return set_err(c, MR_E_INVAL, "unknown routing flags 0x%x", flags);
+  int rc = check_io_align(c, nullptr, nullptr, idx, w, logits);
+  if (rc) return rc;
   if (T == 0) return MR_OK;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
-  int rc = bind(c);
-  if (rc) return rc;
+  if ((rc = bind(c))) return rc;
   hipError_t e = mr::launch_topk(c->launch(), logits, T, E, k, flags, idx, w);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "topk launch");
 }
@@ -604,6 +629,7 @@ int mr_moe_experts(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, con
   int rc = check_layer(c, L);
   if (rc) return rc;
   if (!x || !idx || !w || !y) return set_err(c, MR_E_INVAL, "NULL x, idx, w or y");
+  if ((rc = check_io_align(c, x, y, idx, w, nullptr))) return rc;
   if (T == 0) return MR_OK;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
@@ -654,9 +680,8 @@ int mr_moe_forward(mr_ctx* c, const mr_layer* L, const float* x, float* y) {
   int rc = check_layer(c, L);
   if (rc) return rc;
   if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u)
-    return set_err(c, MR_E_INVAL, "x and y must be 16-byte aligned");
   return forward_one(c, L, x, y, mr::NormResid{});
 }
 
@@ -667,9 +692,9 @@ int mr_moe_forward_residual(mr_ctx* c, const mr_layer* L, const float* h, const 
   if (rc) return rc;
   if (!h || !norm_w || !h_out) return set_err(c, MR_E_INVAL, "NULL h, norm_w or h_out");
   if (!(eps >= 0.f) || eps > 1.f) return set_err(c, MR_E_INVAL, "eps %g is not in [0, 1]", (double)eps);
-  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(h_out)) & 15u)
     return set_err(c, MR_E_INVAL, "h, norm_w and h_out must be 16-byte aligned");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   mr::NormResid nr;
   nr.w = norm_w, nr.eps = eps, nr.resid = h;
   return forward_one(c, L, h, h_out, nr);
@@ -680,6 +705,7 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
   int rc = check_layer(c, L);
   if (rc) return rc;
   if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
   if (T == 0) return MR_OK;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;

@@ -586,6 +586,45 @@ unsigned long long* g_fused_trace = nullptr;
 extern "C" void mr_debug_fused_trace(void* dev_buf) { g_fused_trace = (unsigned long long*)dev_buf; }
 #endif
 
+// Grid of a launch: R routers, ND down groups, NG gate/up units and NS split halves.
+// Workgroups go to CUs round robin (workgroup b on CU b mod n_cu, three per CU). With
+// more than 2 n_cu down and gate/up units, the CUs of the third round that also hold a
+// down group carry three units; splitting those down groups in halves, the second half
+// in a third-round slot on a CU with two units, caps every CU at 2.5 units.
+struct FusedGrid {
+  int R, ND, NG, NS;
+  int total() const { return R + ND + NG + NS; }
+};
+static FusedGrid fused_grid(const mr_layer& L, int n_cu) {
+  FusedGrid g;
+  g.R = (int)((L.E + 3) / 4);
+  g.NG = (int)(L.d.top_k * (L.I / 32));
+  g.ND = (int)((L.H + 15) / 16);
+  const int grid0 = g.R + g.ND + g.NG;
+  g.NS = std::max(0, std::min({g.ND + g.NG - 2 * n_cu, g.ND, 3 * n_cu - grid0, kMaxGrid - grid0}));
+  return g;
+}
+// Dynamic LDS of a launch: the gate/up role's x image (nbH blocks), the down role's four
+// padded slot images, then the 4-byte scale words.
+static uint64_t fused_lds_img_bytes(const mr_layer& L) {
+  return std::max<uint64_t>((L.H / 32) * kImgBytes, 4ull * kImgVec * 1024);
+}
+static uint64_t fused_lds_bytes(const mr_layer& L) {
+  return fused_lds_img_bytes(L) + std::max<uint64_t>(L.H / 32, 4ull * 128) * 4;
+}
+
+// Every workgroup of a launch must be resident at once (workgroups wait on each other):
+// the occupancy the runtime reports for this kernel's registers and LDS, on an otherwise
+// idle device, times the CU count must cover the grid (both instantiations).
+bool fused_resident(const mr_layer& L, int n_cu) {
+  const size_t lds = fused_lds_bytes(L);
+  int b0 = 0, b1 = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, k_fused_mxfp4<false>, 256, lds) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, k_fused_mxfp4<true>, 256, lds) != hipSuccess)
+    return false;
+  return (int64_t)std::min(b0, b1) * n_cu >= fused_grid(L, n_cu).total();
+}
+
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
                         const NormResid& nr) {
@@ -602,28 +641,19 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.dsc = reinterpret_cast<uint32_t*>(img_base + k * nbI * kImgBytes);
   a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k;
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
-  a.R = (int)((L.E + 3) / 4);
-  a.NG = (int)(k * nbI);
-  a.ND = (int)((L.H + 15) / 16);
-  // Workgroups go to CUs round robin (workgroup b on CU b mod n_cu, three per CU). With
-  // more than 2 n_cu down and gate/up units, the CUs of the third round that also hold a
-  // down group carry three units; splitting those down groups in halves, the second half
-  // in a third-round slot on a CU with two units, caps every CU at 2.5 units.
-  const int grid0 = a.R + a.ND + a.NG;
-  a.NS = std::max(0, std::min({a.ND + a.NG - 2 * n_cu, a.ND, 3 * n_cu - grid0, kMaxGrid - grid0}));
+  const FusedGrid fg = fused_grid(L, n_cu);
+  a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS;
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
-  // gate/up: x image (nbH blocks); down: one padded slot image per wave
-  const uint64_t img_bytes = std::max<uint64_t>(nbH * kImgBytes, 4ull * kImgVec * 1024);
-  const uint64_t sc_words = std::max<uint64_t>(nbH, 4ull * 128);
-  a.lds_img_bytes = (uint32_t)img_bytes;
-  const size_t lds = img_bytes + sc_words * 4;
+  a.lds_img_bytes = (uint32_t)fused_lds_img_bytes(L);
+  const size_t lds = fused_lds_bytes(L);
+  (void)nbH;
   ProfScope ps(K, "fused_layer");
   if (nr.w)
-    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(grid0 + a.NS), dim3(256), lds, K.s, a);
+    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(fg.total()), dim3(256), lds, K.s, a);
   else
-    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(grid0 + a.NS), dim3(256), lds, K.s, a);
+    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(fg.total()), dim3(256), lds, K.s, a);
   return hipGetLastError();
 }
 

@@ -493,10 +493,12 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen
   // mode; exp is monotonic, so the order differs only where two logits round to the
   // same probability (a tie by value, which the tests treat as ambiguous).
+  // Keys: + 0.f makes -0.0 and +0.0 share a key; a NaN takes key 1, below every number
+  // (-inf is 0x007FFFFF) and above the absent entries past E (key 0), the order of k_topk.
   uint32_t key[kRouteVals];
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j)  // + 0.f: -0.0 and +0.0 compare equal, so share a key
-    key[j] = (lane + 64 * j < rc.E) ? order_key(v[j] + 0.f) : 0u;
+  for (int j = 0; j < kRouteVals; ++j)
+    key[j] = (lane + 64 * j < rc.E) ? (v[j] == v[j] ? order_key(v[j] + 0.f) : 1u) : 0u;
   RTRACE(3);
   int idx[kRouteVals];
 #pragma unroll

@@ -610,6 +610,19 @@ bool fused_q4k_supported(const mr_layer& L, int n_cu) {
   return true;
 }
 
+// Every workgroup of a launch must be resident at once (workgroups wait on each other):
+// the occupancy the runtime reports for this kernel's registers and LDS, on an otherwise
+// idle device, times the CU count must cover the grid (both instantiations).
+bool fused_q4k_resident(const mr_layer& L, int n_cu) {
+  const uint64_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + has_sh;
+  const int64_t grid = (int64_t)((L.E + has_sh + 3) / 4 + L.H / 8 + ktot * (L.I / 16));
+  int b0 = 0, b1 = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, k_fused_q4k<false>, 256, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, k_fused_q4k<true>, 256, 0) != hipSuccess)
+    return false;
+  return (int64_t)std::min(b0, b1) * n_cu >= grid;
+}
+
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
                             uint8_t* img_base, const NormResid& nr) {
   Q4Args a{};

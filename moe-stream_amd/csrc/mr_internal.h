@@ -91,6 +91,11 @@ struct mr_ctx {
   bool fused_used = false;
   std::string err;
   mr::Scratch scratch;
+  // Scratch allocations superseded by a larger one. Graphs captured earlier keep their
+  // addresses, so these stay allocated (and their fused-kernel error words are still
+  // checked by mr_sync) until mr_ctx_destroy.
+  std::vector<void*> retired;
+  std::vector<uint32_t*> retired_err;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool capturing = false;
   mr::Prof prof;
@@ -178,6 +183,7 @@ struct NormResid {
 // Fused single-launch MXFP4 decode layer (mr_fused.hip).
 constexpr int kSyncErrWord = 96;  // uint32 index of the fused kernel's error word
 bool fused_supported(const mr_layer& L, int n_cu);
+bool fused_resident(const mr_layer& L, int n_cu);      // the whole grid fits the CUs at once
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
                         const NormResid& nr = NormResid{});
@@ -202,6 +208,7 @@ bool grouped_supported(const mr_layer& L);
 hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
                           const float* w, float* y, const GroupedScratch& gs);
 bool fused_q4k_supported(const mr_layer& L, int n_cu);
+bool fused_q4k_resident(const mr_layer& L, int n_cu);
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
                             uint8_t* img_base, const NormResid& nr = NormResid{});
 #ifdef MR_FUSED_TRACE

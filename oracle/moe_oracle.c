@@ -248,6 +248,15 @@ static void f32_matvec_mt(const float* w, const float* x, size_t out_features, s
 
 /* ---- routing: layer.rs:2346-2403 top_k_routing ---------------------------- */
 
+/* a ranks above b in the descending order: the larger number; a NaN ranks below every
+ * number (the reference's partial_cmp -> Equal makes NaN order depend on its sort
+ * algorithm, so this build fixes one rule for all paths). */
+static int ranks_above(float a, float b) {
+  if (isnan(a)) return 0;
+  if (isnan(b)) return 1;
+  return a > b;
+}
+
 /* First k entries of a stable descending sort (Rust sort_by with
  * b.partial_cmp(a), layer.rs:2358/2380): repeatedly take the largest
  * remaining value, ties resolved to the lower index. */
@@ -259,7 +268,7 @@ static void stable_desc_topk(const float* v, size_t n, size_t k, uint32_t* out_i
     size_t best = (size_t)-1;
     for (size_t i = 0; i < n; ++i) {
       if (tk[i]) continue;
-      if (best == (size_t)-1 || v[i] > v[best]) best = i;
+      if (best == (size_t)-1 || ranks_above(v[i], v[best])) best = i;
     }
     tk[best] = 1;
     out_idx[r] = (uint32_t)best;

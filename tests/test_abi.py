@@ -186,3 +186,34 @@ def test_forward_residual_validation(hctx):
     with pytest.raises(M.MoeRocmError) as ei:
         L.forward_residual(0x1000, 0x2000, 1e-6, 0x1000)  # valid (in place): needs a device
     assert ei.value.status == M.MR_E_NODEV
+
+
+def test_alignment_is_checked_before_the_device(hctx):
+    """Kernels read activations and router rows as 16-byte vectors and index/weight arrays
+    as 4-byte words: every entry point rejects misaligned pointers with MR_E_INVAL."""
+    g, u, d = _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 64, 128), _mx_pack(hctx, 4, 128, 64)
+    with pytest.raises(M.MoeRocmError) as ei:
+        M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x1004, route_flags=1, act=1)
+    assert ei.value.status == M.MR_E_INVAL and "16-byte" in ei.value.message
+    with pytest.raises(M.MoeRocmError) as ei:
+        M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x1000, down_bias=0x2008, route_flags=1, act=1)
+    assert ei.value.status == M.MR_E_INVAL
+    L = M.MoeLayer(hctx, g, u, d, top_k=2, router_w=0x1000, route_flags=1, act=1)
+    calls = [
+        lambda: L.forward(0x1004, 0x2000),
+        lambda: L.forward_batched(0x1008, 3, 0x2000),
+        lambda: L.forward_batched(0x1000, 3, 0x2004),
+        lambda: L.experts(0x1004, 2, 0x2000, 0x3000, 0x4000),
+        lambda: L.experts(0x1000, 2, 0x2002, 0x3000, 0x4000),
+        lambda: L.router_topk(0x100c, 2, 0x2000, 0x3000),
+        lambda: L.router_topk(0x1000, 2, 0x2000, 0x3001),
+        lambda: M.topk(hctx, 0x1002, 1, 32, 4, 1, 0x2000, 0x3000),
+    ]
+    for i, call in enumerate(calls):
+        with pytest.raises(M.MoeRocmError) as ei:
+            call()
+        assert ei.value.status == M.MR_E_INVAL, i
+    with pytest.raises(M.MoeRocmError) as ei:  # aligned: validation passes, then no device
+        L.forward_batched(0x1000, 3, 0x2000)
+    assert ei.value.status == M.MR_E_NODEV
+    L.close()

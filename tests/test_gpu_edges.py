@@ -1,0 +1,98 @@
+"""Edge cases of the C ABI on the GPU: scratch growth after a graph was captured, and NaN
+router logits (ranked below every number on every path)."""
+import numpy as np
+import pytest
+
+import moe_rocm as M
+import oracle
+from moe_rocm import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def test_graph_survives_scratch_growth(gpu_ctx):
+    """A graph captured while the context scratch was sized for one token keeps working after
+    a larger batched call grows the scratch (the superseded allocation is kept until the
+    context is destroyed, since the graph still addresses it)."""
+    spec = W.LayerSpec(220, 0, W.GGML_MXFP4, 512, 384, 8, 2, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                       W.ACT_SWIGLU_OAI, True, True)
+    ctx = M.Context(0)  # a fresh context: its scratch starts at this layer's one-token size
+    dl = W.DeviceLayer(ctx, spec)
+    try:
+        dl.layer.reserve(1)
+        x = W.x_tokens(spec, 64, first_token=5)
+        dx1, dy_e, dy_g = ctx.to_device(x[0]), ctx.alloc(spec.hidden * 4), ctx.alloc(spec.hidden * 4)
+        dl.layer.forward(dx1, dy_e)
+        eager = dy_e.download(np.float32)
+        ctx.graph_begin()
+        dl.layer.forward(dx1, dy_g)
+        g = ctx.graph_end()
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(dy_g.download(np.float32), eager)
+        # 64 tokens: the scratch grows (new allocation); the graph still points at the old one
+        dxb, dyb = ctx.to_device(x), ctx.alloc(64 * spec.hidden * 4)
+        dl.layer.forward_batched(dxb, 64, dyb)
+        for _ in range(3):
+            ctx.check(M.lib.mr_dev_zero(ctx.h, dy_g.ptr, spec.hidden * 4))
+            g.launch()
+            dl.layer.forward(dx1, dy_e)  # eager work on the new scratch in between
+            ctx.sync()
+            assert np.array_equal(dy_g.download(np.float32), eager)
+            assert np.array_equal(dy_e.download(np.float32), eager)
+        g.close()
+        for b in (dx1, dy_e, dy_g, dxb, dyb):
+            b.free()
+    finally:
+        dl.close()
+        ctx.close()
+
+
+NAN_SPECS = {
+    "mxfp4-E32": W.LayerSpec(221, 0, W.GGML_MXFP4, 512, 256, 32, 4, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                             W.ACT_SWIGLU_OAI, True, True),
+    "q4k-E300-softmax-after": W.LayerSpec(222, 0, W.GGML_Q4_K, 256, 256, 300, 10, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                                          W.ACT_SILU, False, True),
+}
+
+
+@pytest.mark.parametrize("name", list(NAN_SPECS))
+@pytest.mark.parametrize("kernel", ["fused", "valu"])
+def test_nan_logits_rank_below_every_number(gpu_ctx, name, kernel):
+    """Router logits set through a zero router matrix and the bias, with NaN at the experts
+    that would otherwise rank first: no path selects a NaN expert while numbers remain,
+    and the output matches the oracle (which applies the same rule)."""
+    spec = NAN_SPECS[name]
+    E, k = spec.n_experts, spec.top_k
+    host = W.host_layer(spec)
+    host["router_w"] = np.zeros_like(host["router_w"])
+    b = (-1.0 - np.arange(E, dtype=np.float32) / E)[np.random.default_rng(3).permutation(E)].astype(np.float32)
+    top = np.argsort(-b, kind="stable")[:3]
+    b[top] = np.nan
+    host["router_b"] = b
+    finite = np.where(~np.isnan(b))[0]
+    want = sorted(finite[np.argsort(-b[finite], kind="stable")[:k]].tolist())
+    dl = W.DeviceLayer(gpu_ctx, spec, host=host)
+    L = oracle.layer_from_host(host)
+    x = W.x_tokens(spec, 1, first_token=9)
+    dx, dy = gpu_ctx.to_device(x[0]), gpu_ctx.alloc(spec.hidden * 4)
+    try:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_FUSED if kernel == "fused" else M.DECODE_VALU)
+        dl.layer.forward(dx, dy)
+        gpu_ctx.sync()
+        ry, ridx, _, _ = L.forward(x)
+        assert sorted(ridx[0].tolist()) == want
+        y = dy.download(np.float32)
+        assert np.all(np.isfinite(y))
+        assert rel_err(y, ry[0]) <= REL_TOL
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+        dl.close()
+        dx.free(), dy.free()
