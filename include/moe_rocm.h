@@ -205,6 +205,18 @@ int mr_moe_forward_residual(mr_ctx* ctx, const mr_layer* layer, const float* h, 
  * Replaces the multi-token paths layer.rs:1449-1514 and 2148-2183. */
 int mr_moe_forward_batched(mr_ctx* ctx, const mr_layer* layer, const float* x,
                            uint32_t n_tokens, float* y);
+/* mr_moe_forward_batched without any allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, serving
+ * loops or harnesses that forbid hipMalloc). The same kernels and results, with their
+ * scratch in a static device array of MR_STATIC_SCRATCH_BYTES that every GPU holds for
+ * the life of the process (its address is looked up once per device by mr_ctx_create).
+ * Calls whose scratch would not fit return MR_E_INVAL with the size in mr_last_error
+ * (at the GPT-OSS shape, 64 MiB holds about 600 tokens per call). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (several contexts or streams,
+ * or several host threads) race and must be serialised by the caller. */
+#define MR_STATIC_SCRATCH_BYTES (64ull << 20)
+int mr_moe_forward_batched_noalloc(mr_ctx* ctx, const mr_layer* layer, const float* x,
+                                   uint32_t n_tokens, float* y);
 
 /* ---- GGUF files (gguf/reader.rs; preload of engine.rs:1079-1255) ----------------- */
 /* Opens and memory-maps a GGUF v2/v3 file and parses its header, metadata and

@@ -129,6 +129,32 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   return p;
 }
 
+// Scratch of one batched call (mr_moe_forward_batched_noalloc): routing outputs, logits and
+// router partials, then either the grouped MFMA path's pair lists and images, or the VALU
+// path's activations [T, k, I] and shared activations [T, Ish + 1].
+struct BatchedPlan {
+  uint64_t idx, w, logits, rpart, work, work_sh, total;
+};
+
+BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish, bool grouped) {
+  BatchedPlan p{};
+  uint64_t o = 0;
+  p.idx = o, o += align_up(T * k * 4);
+  p.w = o, o += align_up(T * k * 4);
+  p.logits = o, o += align_up(T * E * 4);
+  p.rpart = o, o += align_up(4 * T * E * 4);
+  p.work = o;
+  if (grouped) {
+    o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
+    p.work_sh = o;
+  } else {
+    o += align_up(T * k * I * 4);
+    p.work_sh = o, o += align_up(T * (Ish + 1) * 4);
+  }
+  p.total = o;
+  return p;
+}
+
 int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
   mr::Scratch& s = c->scratch;
   uint64_t k = L->d.top_k, E = L->E, I = L->I, H = L->H, Ish = L->Ish;
@@ -260,6 +286,9 @@ int mr_ctx_create(int device, mr_ctx** out) {
   }
   c->device = device;
   c->own_stream = true;
+  // the device's static scratch (mr_moe_forward_batched_noalloc), resolved once per device
+  // with the device current; a failure is reported by that entry point only
+  c->static_err = mr::static_scratch_init(device, &c->static_scratch);
   *out = c;
   return MR_OK;
 }
@@ -719,6 +748,45 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
       e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
   }
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch");
+}
+
+int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
+  if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
+  if (T == 0) return MR_OK;
+  const bool grouped = c->decode_kernel != MR_DECODE_VALU && mr::grouped_supported(*L);
+  const BatchedPlan p = plan_batched(T, L->d.top_k, L->E, L->I, L->H, L->Ish, grouped);
+  if (p.total > mr::kStaticScratchBytes)
+    return set_err(c, MR_E_INVAL,
+                   "n_tokens %u needs %llu bytes of scratch at this layer shape; the static scratch holds %llu "
+                   "bytes (use mr_moe_forward_batched, or fewer tokens per call)",
+                   T, (unsigned long long)p.total, (unsigned long long)mr::kStaticScratchBytes);
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if (!c->static_scratch) return hip_fail(c, c->static_err, "static scratch lookup (hipGetSymbolAddress)");
+  if ((rc = bind(c))) return rc;
+  char* b = static_cast<char*>(c->static_scratch);
+  int32_t* idx = reinterpret_cast<int32_t*>(b + p.idx);
+  float* w = reinterpret_cast<float*>(b + p.w);
+  float* logits = reinterpret_cast<float*>(b + p.logits);
+  float* rpart = reinterpret_cast<float*>(b + p.rpart);
+  // no profiling events here: recording them could create events (an allocation)
+  const mr::Launch K{c->stream, nullptr};
+  hipError_t e = mr::launch_router_topk(K, *L, x, T, logits, rpart, idx, w);
+  if (e == hipSuccess) {
+    if (grouped) {
+      mr::Scratch view{};
+      view.grouped = b + p.work;
+      e = mr::launch_grouped(K, *L, x, T, idx, w, y,
+                             mr::grouped_scratch(view, T, L->d.top_k, L->E, L->I, L->H));
+    } else {
+      e = mr::launch_experts_valu(K, *L, x, T, idx, w, reinterpret_cast<float*>(b + p.work),
+                                  reinterpret_cast<float*>(b + p.work_sh), y);
+    }
+  }
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch (static scratch)");
 }
 
 int mr_graph_begin(mr_ctx* c) {

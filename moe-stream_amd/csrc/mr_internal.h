@@ -15,6 +15,8 @@ namespace mr {
 constexpr uint32_t kMaxTopK = 16;        // softmax_topk_kernel limit (fused_ops.metal:150)
 constexpr uint32_t kMaxExperts = 512;    // same limit (fused_ops.metal:158)
 constexpr uint32_t kMaxHidden = 16384;   // LDS-staged activation limit of the VALU kernels
+// Size of the static scratch array of mr_moe_forward_batched_noalloc (one per GPU).
+constexpr uint64_t kStaticScratchBytes = MR_STATIC_SCRATCH_BYTES;
 
 // Per-context scratch: routing outputs, intermediate activations, sync words.
 // Sized by mr_reserve (or lazily on first use outside graph capture).
@@ -96,6 +98,10 @@ struct mr_ctx {
   // checked by mr_sync) until mr_ctx_destroy.
   std::vector<void*> retired;
   std::vector<uint32_t*> retired_err;
+  // This device's static scratch array (mr_moe_forward_batched_noalloc), resolved at
+  // mr_ctx_create; nullptr with static_err set when the lookup failed.
+  void* static_scratch = nullptr;
+  hipError_t static_err = hipSuccess;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool capturing = false;
   mr::Prof prof;
@@ -166,6 +172,9 @@ hipError_t launch_rms_norm(const Launch& K, const float* h, const float* w, floa
                            float* out);
 hipError_t launch_residual_add(const Launch& K, const float* h, const float* m, uint64_t n, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+// With `device` current: this device's address of the static scratch array (looked up once
+// per device).
+hipError_t static_scratch_init(int device, void** out);
 
 // Records an error on the context (or the calling thread when ctx is NULL); returns code.
 int set_error(mr_ctx* ctx, int code, const char* msg);

@@ -91,6 +91,7 @@ _SIGS = {
     "mr_moe_forward": (C.c_int, [_vp, _vp, _vp, _vp]),
     "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
+    "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "mr_gguf_close": (None, [_vp]),
     "mr_gguf_n_tensors": (_u64, [_vp]),
@@ -359,6 +360,11 @@ class MoeLayer:
 
     def forward_batched(self, x, n_tokens: int, y) -> None:
         self.ctx.check(_lib.mr_moe_forward_batched(self.ctx.h, self.h, _ptr(x), n_tokens, _ptr(y)))
+
+    def forward_batched_noalloc(self, x, n_tokens: int, y) -> None:
+        """mr_moe_forward_batched_noalloc: the same result with the static per-GPU scratch
+        (no allocation; calls that overlap on one GPU race)."""
+        self.ctx.check(_lib.mr_moe_forward_batched_noalloc(self.ctx.h, self.h, _ptr(x), n_tokens, _ptr(y)))
 
     def close(self) -> None:
         if self.h:
