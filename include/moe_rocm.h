@@ -68,7 +68,6 @@ extern "C" {
 #define MR_DECODE_VALU 1   /* vector-ALU dequant-matvec kernels, one launch per step */
 #define MR_DECODE_FUSED 2  /* single fused launch per layer: router, top-k, experts, combine
                               (MXFP4 on scaled MX-fp4 MFMA; Q4_K on int8 dot products) */
-#define MR_DECODE_MFMA MR_DECODE_FUSED /* earlier name of MR_DECODE_FUSED */
 /* 1: record a HIP event pair around every kernel launch (read with mr_profile_read). */
 #define MR_OPT_PROFILE 2
 /* Iteration limit of the fused decode kernel's cross-workgroup waits (default

@@ -3,8 +3,9 @@
 // These kernels are the straightforward decode path: one launch per step
 // (router GEMV, top-k, gate+up+SwiGLU, down+combine), one wave per output
 // row, activations staged in LDS. They are the correctness baseline the fused
-// MFMA decode kernel (mr_mfma.hip) is checked and timed against, and they run
-// every layout the ABI accepts (MXFP4 and Q4_K, any H, I multiple of the block).
+// decode kernels (mr_fused.hip, mr_fused_q4k.hip) are checked and timed against,
+// and they run every layout the ABI accepts (MXFP4 and Q4_K, any H, I multiple of
+// the block).
 #include "mr_device.h"
 #include "mr_fused_common.h"
 #include "mr_internal.h"

@@ -28,7 +28,6 @@ OPT_DECODE_KERNEL = 1
 OPT_PROFILE = 2
 OPT_SPIN_LIMIT = 3
 DECODE_AUTO, DECODE_VALU, DECODE_FUSED = 0, 1, 2
-DECODE_MFMA = DECODE_FUSED  # earlier name
 
 if not LIB_PATH.exists():
     raise ImportError(

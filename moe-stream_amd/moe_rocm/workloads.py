@@ -362,3 +362,41 @@ class DecodeStack:
                 b.free()
         for dl in self.layers:
             dl.close()
+
+
+class ChainStack(DecodeStack):
+    """Decode with the hidden state carried from layer to layer: token t starts from h[t] and
+    every layer applies h <- h + moe_l(rms_norm(h, norm_w[l])) in place with one
+    mr_moe_forward_residual (layer.rs:462-473 per layer), so each layer reads what the
+    previous one wrote and the layer order is enforced by the data. Layers are linked in a
+    ring as in DecodeStack; one HIP graph per token."""
+
+    def __init__(self, ctx, specs, *, prefetch_hint: bool = True):
+        super().__init__(ctx, specs, residual=True, prefetch_hint=prefetch_hint)
+
+    def inputs(self, n_tokens: int, first_token: int = 0) -> np.ndarray:
+        """h[token] ~ N(0,1) (the first layer's input stream)."""
+        return x_tokens(self.specs[0], n_tokens, first_token)
+
+    def load(self, xs: np.ndarray) -> None:
+        """Uploads h[token] into the buffers the chain updates in place (kept: h0)."""
+        for b in (self.d_x, self.d_y):
+            if b is not None:
+                b.free()
+        self.h0 = np.ascontiguousarray(xs, dtype=np.float32)
+        self.n_tokens = self.h0.shape[0]
+        self.d_x = self.ctx.to_device(self.h0)
+        self.d_y = None
+        self.ctx.sync()
+
+    def h_ptr(self, t: int) -> int:
+        return self.d_x.ptr + t * self.H * 4
+
+    def enqueue_token(self, t: int) -> None:
+        h = self.h_ptr(t)
+        for li, dl in enumerate(self.layers):
+            dl.layer.forward_residual(h, self.d_nw.ptr + li * self.H * 4, self.eps, h)
+
+    def outputs(self) -> np.ndarray:
+        """h[token] after the whole stack."""
+        return self.d_x.download(np.float32).reshape(self.n_tokens, self.H)

@@ -69,3 +69,41 @@ def test_timed_pipeline_matches_oracle(gpu_ctx, residual):
                     assert err <= REL_TOL, (rep, t, li, err)
     finally:
         stack.close()
+
+
+def test_chained_pipeline_matches_eager_chain_and_oracle(gpu_ctx):
+    """bench.py --decode chain: one hidden state per token carried through four C2 layers in
+    place (mr_moe_forward_residual per layer), the layers in a set_next ring, one graph per
+    token. The replayed graphs must leave exactly the bits of the same chain run eagerly;
+    each layer of the eager chain is then compared with the oracle on its own input (the
+    chain amplifies rounding differences from layer to layer, so whole-chain errors of two
+    correct implementations are not comparable)."""
+    specs = W.config_layers(2)[:N_LAYERS]
+    stack = W.ChainStack(gpu_ctx, specs)
+    H = stack.H
+    try:
+        h0 = stack.inputs(N_TOKENS, first_token=700)
+        stack.load(h0)
+        stack.capture()
+        for t in range(N_TOKENS):
+            stack.run(t)
+        gpu_ctx.sync()
+        got = stack.outputs()
+        orc = _oracle_layers(stack)
+        buf = gpu_ctx.alloc(H * 4)
+        try:
+            for t in range(N_TOKENS):
+                buf.upload(h0[t])
+                for li, dl in enumerate(stack.layers):
+                    hin = buf.download(np.float32)
+                    dl.layer.forward_residual(buf, stack.d_nw.ptr + li * H * 4, stack.eps, buf)
+                    out = buf.download(np.float32).astype(np.float64)
+                    ref, _, _, lg = orc[li].forward_residual(hin, stack.norm_w[li], stack.eps, n_threads=8)
+                    if not _tie_ambiguous(lg[0], specs[li].top_k):
+                        err = np.abs(out - ref[0]).max() / np.abs(ref[0].astype(np.float64) - hin).max()
+                        assert err <= REL_TOL, (t, li, err)
+                assert np.array_equal(buf.download(np.float32), got[t]), t
+        finally:
+            buf.free()
+    finally:
+        stack.close()
