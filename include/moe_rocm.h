@@ -204,6 +204,12 @@ int mr_moe_forward_residual(mr_ctx* ctx, const mr_layer* layer, const float* h, 
  * Replaces the multi-token paths layer.rs:1449-1514 and 2148-2183. */
 int mr_moe_forward_batched(mr_ctx* ctx, const mr_layer* layer, const float* x,
                            uint32_t n_tokens, float* y);
+/* mr_moe_forward_batched with the post-attention RMSNorm and the residual add of every token
+ * (layer.rs:462-473 over a [T, H] hidden state, the prefill form of mr_moe_forward_residual):
+ * h_out[t] = h[t] + moe(rms_norm(h[t], norm_w, eps)). h_out may equal h. h, norm_w, h_out
+ * 16-byte aligned; 0 <= eps <= 1. */
+int mr_moe_forward_batched_residual(mr_ctx* ctx, const mr_layer* layer, const float* h, uint32_t n_tokens,
+                                    const float* norm_w, float eps, float* h_out);
 /* mr_moe_forward_batched without any allocation. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture, serving
  * loops or harnesses that forbid hipMalloc). The same kernels and results, with their

@@ -122,7 +122,8 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40);
   p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
-  p.grouped = o, o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
+  p.grouped = o, o += align_up(std::max(mr::grouped_scratch_bytes(T, k, E, I, H),
+                                        mr::grouped_q4k_scratch_bytes(T, k, E, I, H, Ish)));
   p.xn = o, o += align_up(T * H * 4);
   p.ytmp = o, o += align_up(T * H * 4);
   p.total = o;
@@ -136,7 +137,16 @@ struct BatchedPlan {
   uint64_t idx, w, logits, rpart, work, work_sh, total;
 };
 
-BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish, bool grouped) {
+// Which multi-token path a layer takes (mr_moe_forward_batched and its static-scratch variant).
+enum class Batched { valu, grouped_mx, grouped_q4k };
+Batched batched_kind(const mr_ctx* c, const mr_layer& L) {
+  if (c->decode_kernel == MR_DECODE_VALU) return Batched::valu;
+  if (mr::grouped_supported(L)) return Batched::grouped_mx;
+  if (mr::grouped_q4k_supported(L)) return Batched::grouped_q4k;
+  return Batched::valu;
+}
+
+BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish, Batched kind) {
   BatchedPlan p{};
   uint64_t o = 0;
   p.idx = o, o += align_up(T * k * 4);
@@ -144,8 +154,11 @@ BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.logits = o, o += align_up(T * E * 4);
   p.rpart = o, o += align_up(4 * T * E * 4);
   p.work = o;
-  if (grouped) {
+  if (kind == Batched::grouped_mx) {
     o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
+    p.work_sh = o;
+  } else if (kind == Batched::grouped_q4k) {
+    o += align_up(mr::grouped_q4k_scratch_bytes(T, k, E, I, H, Ish));
     p.work_sh = o;
   } else {
     o += align_up(T * k * I * 4);
@@ -729,6 +742,24 @@ int mr_moe_forward_residual(mr_ctx* c, const mr_layer* L, const float* h, const 
   return forward_one(c, L, h, h_out, nr);
 }
 
+// Routing and experts for T tokens (scratch already sized for T): the grouped GEMM path of the
+// layer's type, else the per-token VALU kernels.
+static hipError_t batched_core(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
+  mr::Scratch& s = c->scratch;
+  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, s.logits, s.rpart, s.idx, s.w);
+  if (e == hipSuccess) {
+    const Batched kind = batched_kind(c, *L);
+    if (kind == Batched::grouped_mx)
+      e = mr::launch_grouped(c->launch(), *L, x, T, s.idx, s.w, y,
+                             mr::grouped_scratch(s, s.cap_tokens, s.cap_k, s.cap_e, s.cap_i, s.cap_h));
+    else if (kind == Batched::grouped_q4k)
+      e = mr::launch_grouped_q4k(c->launch(), *L, x, T, s.idx, s.w, y, s.grouped);
+    else
+      e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
+  }
+  return e;
+}
+
 int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   int rc = check_layer(c, L);
@@ -738,16 +769,27 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
   if (T == 0) return MR_OK;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
-  mr::Scratch& s = c->scratch;
-  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, s.logits, s.rpart, s.idx, s.w);
-  if (e == hipSuccess) {
-    if (c->decode_kernel != MR_DECODE_VALU && mr::grouped_supported(*L))
-      e = mr::launch_grouped(c->launch(), *L, x, T, s.idx, s.w, y,
-                             mr::grouped_scratch(s, s.cap_tokens, s.cap_k, s.cap_e, s.cap_i, s.cap_h));
-    else
-      e = mr::launch_experts_valu(c->launch(), *L, x, T, s.idx, s.w, s.act, s.act_sh, y);
-  }
+  const hipError_t e = batched_core(c, L, x, T, y);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch");
+}
+
+int mr_moe_forward_batched_residual(mr_ctx* c, const mr_layer* L, const float* h, uint32_t T, const float* norm_w,
+                                    float eps, float* h_out) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  int rc = check_layer(c, L);
+  if (rc) return rc;
+  if (!h || !norm_w || !h_out) return set_err(c, MR_E_INVAL, "NULL h, norm_w or h_out");
+  if (!(eps >= 0.f) || eps > 1.f) return set_err(c, MR_E_INVAL, "eps %g is not in [0, 1]", (double)eps);
+  if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(h_out)) & 15u)
+    return set_err(c, MR_E_INVAL, "h, norm_w and h_out must be 16-byte aligned");
+  if (T == 0) return MR_OK;
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
+  mr::Scratch& s = c->scratch;
+  hipError_t e = mr::launch_rms_norm(c->launch(), h, norm_w, eps, T, L->H, s.xn);
+  if (e == hipSuccess) e = batched_core(c, L, s.xn, T, s.ytmp);
+  if (e == hipSuccess) e = mr::launch_residual_add(c->launch(), h, s.ytmp, (uint64_t)T * L->H, h_out);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe residual launch");
 }
 
 int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
@@ -757,8 +799,8 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
   if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
   if (T == 0) return MR_OK;
-  const bool grouped = c->decode_kernel != MR_DECODE_VALU && mr::grouped_supported(*L);
-  const BatchedPlan p = plan_batched(T, L->d.top_k, L->E, L->I, L->H, L->Ish, grouped);
+  const Batched kind = batched_kind(c, *L);
+  const BatchedPlan p = plan_batched(T, L->d.top_k, L->E, L->I, L->H, L->Ish, kind);
   if (p.total > mr::kStaticScratchBytes)
     return set_err(c, MR_E_INVAL,
                    "n_tokens %u needs %llu bytes of scratch at this layer shape; the static scratch holds %llu "
@@ -776,11 +818,13 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   const mr::Launch K{c->stream, nullptr};
   hipError_t e = mr::launch_router_topk(K, *L, x, T, logits, rpart, idx, w);
   if (e == hipSuccess) {
-    if (grouped) {
+    if (kind == Batched::grouped_mx) {
       mr::Scratch view{};
       view.grouped = b + p.work;
       e = mr::launch_grouped(K, *L, x, T, idx, w, y,
                              mr::grouped_scratch(view, T, L->d.top_k, L->E, L->I, L->H));
+    } else if (kind == Batched::grouped_q4k) {
+      e = mr::launch_grouped_q4k(K, *L, x, T, idx, w, y, b + p.work);
     } else {
       e = mr::launch_experts_valu(K, *L, x, T, idx, w, reinterpret_cast<float*>(b + p.work),
                                   reinterpret_cast<float*>(b + p.work_sh), y);

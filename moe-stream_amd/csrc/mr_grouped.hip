@@ -466,13 +466,15 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 
 // ---- combine -----------------------------------------------------------------------------
 // y[t][row] = sum over t's pairs in ascending pair index (= ascending expert) of
-// o[pair][row] + w * b_down[e][row]. One thread per (token, 4 rows) on a (row groups, tokens)
-// grid (tokens past gridDim.y loop); the token's (at most KM) pair indices stay in registers and are taken smallest first,
-// and all of a thread's loads issue before the sums. H % 4 == 0.
+// o[pair][row] + w * b_down[e][row], then + sig[t] * o_sh[t][row] when a shared expert ran
+// (layer.rs:1935-1951). One thread per (token, 4 rows) on a (row groups, tokens) grid (tokens
+// past gridDim.y loop); the token's (at most KM) pair indices stay in registers and are taken
+// smallest first, and all of a thread's loads issue before the sums. H % 4 == 0.
 template <int KM>
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, const int32_t* __restrict__ pair_of,
                                                  const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                  const float* __restrict__ down_b, int T, int k, int H,
+                                                 const float* __restrict__ o_sh, const float* __restrict__ sh_sig,
                                                  float* __restrict__ y) {
   const int row = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (row >= H) return;
@@ -499,6 +501,12 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, co
         }
       }
     }
+    f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+    float sg = 0.f;
+    if (o_sh) {
+      sv = *reinterpret_cast<const f32x4*>(o_sh + (size_t)t * H + row);
+      sg = sh_sig[t];
+    }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < KM; ++r) {
@@ -511,6 +519,9 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ o, co
         }
       }
     }
+    if (o_sh)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = acc[c] + sg * sv[c];
     *reinterpret_cast<f32x4*>(y + (size_t)t * H + row) = acc;
   }
 }
@@ -566,18 +577,45 @@ bool grouped_supported(const mr_layer& L) {
          L.E <= 1024 && L.H <= 4u * 32 * kMaxSteps && L.I <= 4u * 32 * kMaxSteps;
 }
 
+hipError_t launch_group(const Launch& K, const int32_t* idx, const float* w, int P, int k, int E, int32_t* pair_tok,
+                        float* pair_w, int32_t* pair_of, int32_t* exp_off, int32_t* tile_off) {
+  ProfScope ps(K, "group");
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(256), 0, K.s, idx, w, P, k, E, pair_tok, pair_w, pair_of, exp_off,
+                     tile_off);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const Launch& K, const float* o, const int32_t* pair_of, const int32_t* idx, const float* w,
+                          const float* down_b, uint32_t T, int k, int H, const float* o_sh, const float* sh_sig,
+                          float* y) {
+  ProfScope ps(K, "combine");
+  const dim3 grid((unsigned)((H / 4 + 255) / 256), std::min<uint32_t>(T, 65535u));
+  if (k <= 4)
+    hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, K.s, o, pair_of, idx, w, down_b, (int)T, k, H, o_sh, sh_sig,
+                       y);
+  else if (k <= 8)
+    hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, K.s, o, pair_of, idx, w, down_b, (int)T, k, H, o_sh, sh_sig,
+                       y);
+  else
+    hipLaunchKernelGGL(k_combine<16>, grid, dim3(256), 0, K.s, o, pair_of, idx, w, down_b, (int)T, k, H, o_sh,
+                       sh_sig, y);
+  return hipGetLastError();
+}
+
+// Workgroups for a grouped GEMM of at most `items` work items: a multiple of the XCD count, so
+// that every XCD's contiguous range of ceil(n_work / 8) items has a workgroup for each item
+// (workgroup b takes item (b mod 8) * ceil(n_work / 8) + b / 8).
+unsigned grouped_grid(uint64_t items) { return (unsigned)((items + kXcds - 1) / kXcds * kXcds); }
+
 hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
                           const float* w, float* y, const GroupedScratch& gs) {
   const int k = (int)L.d.top_k, E = (int)L.E, H = (int)L.H, I = (int)L.I;
   const int P = (int)T * k;
   const int max_tiles = (P + kPairTile - 1) / kPairTile + E;
   hipError_t e;
-  {
-    ProfScope ps(K, "group");
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(256), 0, K.s, idx, w, P, k, E, gs.pair_tok, gs.pair_w, gs.pair_of,
-                       gs.exp_off, gs.tile_off);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
+  if ((e = launch_group(K, idx, w, P, k, E, gs.pair_tok, gs.pair_w, gs.pair_of, gs.exp_off, gs.tile_off)) !=
+      hipSuccess)
+    return e;
   {
     ProfScope ps(K, "split_x");
     hipLaunchKernelGGL(k_split_rows, dim3((unsigned)((H / 32 + 31) / 32), std::min<uint32_t>(T, 65535u)), dim3(256), 0,
@@ -594,7 +632,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   {
     ProfScope ps(K, "grouped_gateup");
     constexpr int rows = (kGW / 2) * kGT * 16;
-    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3((unsigned)(((I + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
+    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3(grouped_grid((uint64_t)((I + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
                        K.s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -606,25 +644,11 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   {
     ProfScope ps(K, "grouped_down");
     constexpr int rows = kGW * kGT * 16;
-    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3((unsigned)(((H + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
+    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3(grouped_grid((uint64_t)((H + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
                        K.s, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  {
-    ProfScope ps(K, "combine");
-    const dim3 grid((unsigned)((H / 4 + 255) / 256), std::min<uint32_t>(T, 65535u));
-    if (k <= 4)
-      hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
-                         H, y);
-    else if (k <= 8)
-      hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
-                         H, y);
-    else
-      hipLaunchKernelGGL(k_combine<16>, grid, dim3(256), 0, K.s, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, (int)T, k,
-                         H, y);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  return hipSuccess;
+  return launch_combine(K, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, T, k, H, nullptr, nullptr, y);
 }
 
 }  // namespace mr

@@ -216,6 +216,20 @@ uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, u
 bool grouped_supported(const mr_layer& L);
 hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
                           const float* w, float* y, const GroupedScratch& gs);
+// Pair grouping, grid size and the ascending-expert combine shared by the grouped paths
+// (mr_grouped.hip).
+unsigned grouped_grid(uint64_t items);
+hipError_t launch_group(const Launch& K, const int32_t* idx, const float* w, int P, int k, int E, int32_t* pair_tok,
+                        float* pair_w, int32_t* pair_of, int32_t* exp_off, int32_t* tile_off);
+hipError_t launch_combine(const Launch& K, const float* o, const int32_t* pair_of, const int32_t* idx, const float* w,
+                          const float* down_b, uint32_t T, int k, int H, const float* o_sh, const float* sh_sig,
+                          float* y);
+// Grouped multi-token Q4_K path on the int8 MFMA (mr_grouped_q4k.hip); scratch: one block of
+// grouped_q4k_scratch_bytes.
+bool grouped_q4k_supported(const mr_layer& L);
+uint64_t grouped_q4k_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish);
+hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
+                              const float* w, float* y, void* scratch);
 bool fused_q4k_supported(const mr_layer& L, int n_cu);
 bool fused_q4k_resident(const mr_layer& L, int n_cu);
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,

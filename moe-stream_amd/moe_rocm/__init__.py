@@ -90,6 +90,7 @@ _SIGS = {
     "mr_moe_forward": (C.c_int, [_vp, _vp, _vp, _vp]),
     "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
+    "mr_moe_forward_batched_residual": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _f32, _vp]),
     "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "mr_gguf_close": (None, [_vp]),
@@ -359,6 +360,11 @@ class MoeLayer:
 
     def forward_batched(self, x, n_tokens: int, y) -> None:
         self.ctx.check(_lib.mr_moe_forward_batched(self.ctx.h, self.h, _ptr(x), n_tokens, _ptr(y)))
+
+    def forward_batched_residual(self, h, n_tokens: int, norm_w, eps: float, h_out) -> None:
+        """mr_moe_forward_batched_residual: h_out[t] = h[t] + moe(rms_norm(h[t]))."""
+        self.ctx.check(_lib.mr_moe_forward_batched_residual(self.ctx.h, self.h, _ptr(h), n_tokens, _ptr(norm_w),
+                                                            eps, _ptr(h_out)))
 
     def forward_batched_noalloc(self, x, n_tokens: int, y) -> None:
         """mr_moe_forward_batched_noalloc: the same result with the static per-GPU scratch

@@ -208,6 +208,15 @@ extern "C" {
         n_tokens: u32,
         y: *mut f32,
     ) -> c_int;
+    pub fn mr_moe_forward_batched_residual(
+        ctx: *mut mr_ctx,
+        layer: *const mr_layer,
+        h: *const f32,
+        n_tokens: u32,
+        norm_w: *const f32,
+        eps: f32,
+        h_out: *mut f32,
+    ) -> c_int;
     pub fn mr_moe_forward_batched_noalloc(
         ctx: *mut mr_ctx,
         layer: *const mr_layer,
