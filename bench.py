@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--residual", action="store_true",
                     help="time mr_moe_forward_residual (post-attention RMSNorm + MoE + residual add)")
+    ap.add_argument("--batched", type=int, default=0,
+                    help="time mr_moe_forward_batched on layer 0 of --config with this many tokens "
+                         "(C5 is always a batched run, of 512 tokens unless this is given)")
     ap.add_argument("--decode", default="layers", choices=["layers", "chain"],
                     help="layers: every layer reads its own input x[token][layer] (mr_moe_forward); "
                          "chain: one hidden state per token carried through the layers in place, one "
@@ -52,6 +55,12 @@ def parse():
                     help="oracle threads for the CPU baseline (0: every logical core, as the reference's available_parallelism)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel of known size (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--trace", action="store_true",
+                    help="only trace one fused MXFP4 decode launch (layer 5 of a token, --config 1 or 2) with the "
+                         "library built by `python moe-stream_amd/moe_rocm/build.py --trace`: phase times per role")
+    ap.add_argument("--probe", action="store_true",
+                    help="only measure the ceilings: a graph of empty kernels (the kernel-boundary floor) and "
+                         "plain streaming reads of the decode layers' byte counts")
     return ap.parse_args()
 
 
@@ -102,6 +111,146 @@ def copy_calibration(n_bytes: int = 1 << 30, reps: int = 4) -> None:
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration": {"read_bytes": n_bytes, "write_bytes": n_bytes,
                                            "dispatches": reps, "kernel": "torch mul float32"}}))
+
+
+def probes() -> None:
+    """Ceilings of the decode path on this GPU, with the library's probe kernels:
+    - kernel boundary: a HIP graph of 24 empty kernels (as a token's graph holds 24 layer
+      launches) with the C2 fused kernel's grid and with one workgroup, time per kernel;
+    - plain stream: mr_probe_read over the byte count of one C2 layer (53.4 MB), of its gate/up
+      weights (35.2 MB) and of one C3 layer (22.3 MB), with the C2 fused grid's workgroup count
+      and with 2048, reading in turn from 8 buffers (427 MB, beyond the 256 MB Infinity Cache)
+      so that every read comes from HBM."""
+    import moe_rocm as M
+    from moe_rocm import workloads as W
+
+    ctx = M.Context(0)
+    c2 = W.gpt_oss(2, 0)
+    c2_bytes, c3_bytes = c2.weight_bytes_per_token(), W.qwen3_30b(3, 0).weight_bytes_per_token()
+    gu_bytes = c2.top_k * 2 * M.synth.matrix_bytes(c2.ggml_type, c2.inter, c2.hidden)
+    fused_grid = 576  # C2: 8 router + 180 down + 360 gate/up + 28 split down workgroups
+    out = {"probe": "decode ceilings", "gpu_workgroups_c2_fused": fused_grid}
+    floor = {}
+    for n_wg in (fused_grid, 1):
+        ctx.graph_begin()
+        for _ in range(24):
+            ctx.probe_empty(n_wg)
+        g = ctx.graph_end()
+        for _ in range(3):
+            g.launch()
+        ctx.sync()
+        reps = 50
+        ctx.timer_start()
+        for _ in range(reps):
+            g.launch()
+        ms = ctx.timer_stop()
+        g.close()
+        floor[str(n_wg)] = round(ms * 1e3 / (reps * 24), 3)
+    out["empty_kernel_in_graph_us"] = floor
+    n_buf = 8
+    size = (c2_bytes + 4095) // 4096 * 4096
+    bufs = [ctx.alloc(size) for _ in range(n_buf)]
+    for b in bufs:
+        ctx.synth_blocks(M.GGML_MXFP4, b, size // 17, 7)
+    sink = ctx.alloc(4 * 4096)
+    reads = []
+    for name, nbytes in (("c2_layer", c2_bytes), ("c2_gate_up", gu_bytes), ("c3_layer", c3_bytes)):
+        nbytes = nbytes // 16 * 16
+        for n_wg in (fused_grid, 2048):
+            for i in range(n_buf):
+                ctx.probe_read(bufs[i], nbytes, n_wg, sink)
+            ctx.sync()
+            reps = 64
+            ctx.timer_start()
+            for i in range(reps):
+                ctx.probe_read(bufs[i % n_buf], nbytes, n_wg, sink)
+            ms = ctx.timer_stop()
+            us = ms * 1e3 / reps
+            reads.append({"bytes": name, "nbytes": nbytes, "workgroups": n_wg, "us": round(us, 3),
+                          "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    out["plain_read"] = reads
+    for b in bufs + [sink]:
+        b.free()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+def trace_decode(a) -> None:
+    """Phase timestamps of one fused MXFP4 decode launch (device clock, 100 MHz, read at each
+    role's phase boundaries by thread 0 of every workgroup; the first workgroup start is 0).
+    The launch is layer 5 of the seventh token of the bench's layer ring, enqueued eagerly after
+    six tokens through every layer, so its router rows were prefetched by layer 4 as in the timed
+    pipeline. Also the gate/up workgroups' stream time grouped by how many gate/up and down
+    workgroups share their CU (the CU read from the hardware id)."""
+    lib = ROOT / "moe-stream_amd" / "moe_rocm" / "trace" / "libmoe_rocm.so"
+    os.environ.setdefault("MOE_ROCM_LIB", str(lib))
+    import ctypes as C
+
+    import moe_rocm as M
+    from moe_rocm import workloads as W
+
+    if not hasattr(M._lib, "mr_debug_fused_trace"):
+        sys.exit(f"{M.LIB_PATH} has no trace points: build it with `python moe-stream_amd/moe_rocm/build.py --trace`")
+    M._lib.mr_debug_fused_trace.argtypes = [C.c_void_p]
+    ctx = M.Context(0)
+    specs = W.config_layers(a.config)
+    stack = W.DecodeStack(ctx, specs, residual=a.residual)
+    stack.load(stack.inputs(8))
+    for t in range(6):
+        stack.enqueue_token(t)
+    li = 5 % len(specs)
+    s0 = specs[li]
+    R, ND, NG = (s0.n_experts + 3) // 4, (s0.hidden + 15) // 16, s0.top_k * (s0.inter // 32)
+    buf = ctx.zeros((1024 * 32,), dtype=np.uint64)
+    def launch(l):
+        if a.residual:
+            stack.layers[l].layer.forward_residual(stack.x_ptr(6, l), stack.d_nw.ptr + l * stack.H * 4, stack.eps,
+                                                   stack.y_ptr(l))
+        else:
+            stack.layers[l].layer.forward(stack.x_ptr(6, l), stack.y_ptr(l))
+
+    for l in range(li):
+        launch(l)
+    ctx.sync()
+    M._lib.mr_debug_fused_trace(buf.ptr)
+    launch(li)
+    ctx.sync()
+    M._lib.mr_debug_fused_trace(None)
+    tr = buf.download(np.uint64).reshape(1024, 32).astype(np.int64)
+    grid = int(np.count_nonzero(tr[:, 0]))
+    us = (tr[:grid] - tr[:grid, 0].min()) / 100.0
+    role = np.array(["router" if b < R else ("gateup" if R + ND <= b < R + ND + NG else "down") for b in range(grid)])
+
+    def q(v):
+        return {"min": round(float(v.min()), 2), "median": round(float(np.median(v)), 2), "max": round(float(v.max()), 2)}
+
+    phases = {
+        "router": {"start": q(us[role == "router", 0]), "logits_published": q(us[role == "router", 1]),
+                   "exit": q(us[role == "router", 5])},
+        "gateup": {"start": q(us[role == "gateup", 0]), "x_image_built": q(us[role == "gateup", 1]),
+                   "routed": q(us[role == "gateup", 2]), "stream_done": q(us[role == "gateup", 3]),
+                   "epilogue_stored": q(us[role == "gateup", 4]), "exit": q(us[role == "gateup", 5])},
+        "down": {"start": q(us[role == "down", 0]), "routed": q(us[role == "down", 1]),
+                 "weights_prepared": q(us[role == "down", 2]), "gateup_count_seen": q(us[role == "down", 3]),
+                 "image_in_lds": q(us[role == "down", 4]), "exit": q(us[role == "down", 5])},
+    }
+    cu = [(b % 8, int(tr[b, 7])) for b in range(grid)]  # (XCD, hardware CU id); workgroup b runs on XCD b mod 8
+    by_cu = {}
+    for b in range(grid):
+        by_cu.setdefault(cu[b], []).append(b)
+    groups = {}
+    for b in np.nonzero(role == "gateup")[0]:
+        co = by_cu[cu[b]]
+        key = f"{sum(role[c] == 'gateup' for c in co)} gateup + {sum(role[c] == 'down' for c in co)} down"
+        groups.setdefault(key, []).append(us[b, 3] - us[b, 2])
+    out = {"trace": W.CONFIG_NAMES[a.config], "layer": li, "workgroups": grid, "cus": len(by_cu),
+           "kernel_us": round(float(us[:, 5].max()), 2), "phases_us": phases,
+           "gateup_stream_us_by_cu_load": {k: {"workgroups": len(v), "median": round(float(np.median(v)), 2),
+                                               "max": round(float(max(v)), 2)} for k, v in sorted(groups.items())}}
+    print(json.dumps(out), flush=True)
+    buf.free()
+    stack.close()
+    ctx.close()
 
 
 def measured_traffic(config: int):
@@ -222,13 +371,15 @@ def chain_check(ctx, M, stack, t_last: int, kernel_opt: int) -> dict:
 
 
 MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 (the f8f6f4 MFMA with an fp8 B operand)
+MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8
 
 
 def bench_batched(a, ctx, M, W, spec):
-    """C5: one step = one batched forward of 512 tokens through the Zipf-skewed
-    GPT-OSS-shape layer (router, top-4, grouped gate/up + SwiGLU, grouped down,
-    combine)."""
-    T = W.CONFIG_TOKENS[5]
+    """One step = one batched forward of T tokens through one layer (router, top-k, grouped
+    gate/up + activation, grouped down, combine). C5: 512 tokens through the Zipf-skewed
+    GPT-OSS-shape layer; with --batched T on another config: T tokens through its layer 0
+    (Q4_K layers take the grouped int8-MFMA path)."""
+    T = a.batched or W.CONFIG_TOKENS[5]
     K, Wm = a.steps if a.steps != 256 else 20, a.warmup
     dl = W.DeviceLayer(ctx, spec)
     dl.layer.reserve(T)
@@ -261,7 +412,8 @@ def bench_batched(a, ctx, M, W, spec):
     ctx.sync()
     kern = {}
     for name in ("router_logits", "topk", "group", "split_x", "grouped_gateup", "split_h", "grouped_down",
-                 "combine", "gateup", "down"):
+                 "split_q4k", "grouped_q4k_gateup", "grouped_q4k_down", "grouped_q4k_shared_gateup",
+                 "grouped_q4k_shared_down", "shared_gate", "combine", "gateup", "down", "shared_gateup"):
         n, tot = ctx.profile_read(name)
         if n:
             kern[name] = (n, tot)
@@ -270,15 +422,20 @@ def bench_batched(a, ctx, M, W, spec):
     dom = max(kern, key=lambda k: kern[k][1])
     avg_ms = kern[dom][1] / kern[dom][0]
     pairs = T * spec.top_k
-    flops = {"grouped_gateup": 2.0 * pairs * 2 * I * H, "grouped_down": 2.0 * pairs * H * I}
+    flops = {"grouped_gateup": 2.0 * pairs * 2 * I * H, "grouped_down": 2.0 * pairs * H * I,
+             "grouped_q4k_gateup": 2.0 * pairs * 2 * I * H, "grouped_q4k_down": 2.0 * pairs * H * I}
     bytes_step = W.batched_bytes(spec, T)
     roof = None
     if dom in flops:
         ach = flops[dom] / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": MFMA_FP8_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / MFMA_FP8_PEAK_TFLOPS, 4), "traffic": None,
+        q4 = dom.startswith("grouped_q4k")
+        peak = MFMA_INT8_PEAK_TOPS if q4 else MFMA_FP8_PEAK_TFLOPS
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": peak,
+                "unit": "TOP/s" if q4 else "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None,
                 "flops_per_launch": flops[dom], "avg_launch_us": round(avg_ms * 1e3, 2),
-                "note": "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this MFMA work"}
+                "note": ("GEMM ops of the layer; the 2-term int8 activation split issues 2x this MFMA work"
+                         if q4 else "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this "
+                                    "MFMA work")}
     cpu = None
     if not a.no_cpu_baseline:
         import oracle  # test infrastructure; used here only as the timed CPU baseline
@@ -299,13 +456,15 @@ def bench_batched(a, ctx, M, W, spec):
                "host": host_cpu(),
                "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on {ns} of the "
                          f"{T} tokens"}
+    workload = W.CONFIG_NAMES[5] if a.config == 5 else f"{W.CONFIG_NAMES[a.config]}: layer 0, batched {T} tokens"
     out = {
         "metric": "expert-FFN batched/prefill tokens/s + MFMA utilisation, GPT-OSS-20B shape",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(ms / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "mxfp4-weights/e4m3x4-act/f32-acc",
-        "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1); Zipf(1.1) router skew)",
-        "config": {"workload": W.CONFIG_NAMES[5], "config_id": 5, "tokens": T, "hidden": H, "inter": I,
+        "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if spec.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
+        "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1)"
+                + ("; Zipf(1.1) router skew)" if spec.zipf_s else ")"),
+        "config": {"workload": workload, "config_id": a.config, "tokens": T, "hidden": H, "inter": I,
                    "experts": spec.n_experts, "top_k": spec.top_k, "graph": g is not None},
         "hbm_gbs": round(bytes_step * K / (ms / 1e3) / 1e9, 1),
         "hbm_frac": round(bytes_step * K / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -325,6 +484,12 @@ def main():
     if a.copy_calibration:
         copy_calibration()
         return
+    if a.probe:
+        probes()
+        return
+    if a.trace:
+        trace_decode(a)
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the MoE path is measured on "
                           "one MI355X; multi-GPU expert parallelism is a design note, not a run",
@@ -337,7 +502,7 @@ def main():
     kernel_opt = {"auto": M.DECODE_AUTO, "valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel]
     ctx.set_option(M.OPT_DECODE_KERNEL, kernel_opt)
     specs = W.config_layers(a.config)
-    if a.config == 5:
+    if a.config == 5 or a.batched:
         bench_batched(a, ctx, M, W, specs[0])
         return
     n_layers = len(specs)

@@ -308,6 +308,15 @@ int mr_profile_reset(mr_ctx* ctx);
  * Irwin-Hall(12) construction, scale and quant bytes uniform). */
 int mr_synth_blocks(mr_ctx* ctx, int ggml_type, void* dst, uint64_t n_blocks, uint64_t seed);
 
+/* ---- measurement probes (bench support, not a reference interface) ------------ */
+/* A plain streaming read of nbytes (a multiple of 16) from src by n_workgroups workgroups of
+ * 256 threads (16-byte loads, four in flight per thread; one word per workgroup is written to
+ * sink [n_workgroups] u32), and an empty kernel of n_workgroups workgroups: the ceilings the
+ * decode kernels are measured against (the bytes a plain stream moves per microsecond, the
+ * cost of a kernel boundary). Profile names "probe_read" and "probe_empty". */
+int mr_probe_read(mr_ctx* ctx, const void* src, uint64_t nbytes, uint32_t n_workgroups, uint32_t* sink);
+int mr_probe_empty(mr_ctx* ctx, uint32_t n_workgroups);
+
 #ifdef __cplusplus
 }
 #endif

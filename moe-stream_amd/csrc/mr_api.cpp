@@ -833,6 +833,27 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch (static scratch)");
 }
 
+int mr_probe_read(mr_ctx* c, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t* sink) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!src || !sink || n_wg == 0 || nbytes % 16 != 0) return set_err(c, MR_E_INVAL, "probe_read: bad arguments");
+  if (misaligned(src, 16)) return set_err(c, MR_E_INVAL, "probe_read: src must be 16-byte aligned");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  const hipError_t e = mr::launch_probe_read(c->launch(), src, nbytes, n_wg, sink);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_read launch");
+}
+
+int mr_probe_empty(mr_ctx* c, uint32_t n_wg) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (n_wg == 0) return set_err(c, MR_E_INVAL, "probe_empty: n_workgroups is 0");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  const hipError_t e = mr::launch_probe_empty(c->launch(), n_wg);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_empty launch");
+}
+
 int mr_graph_begin(mr_ctx* c) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");

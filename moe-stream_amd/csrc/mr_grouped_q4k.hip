@@ -34,7 +34,6 @@ typedef int i32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kQPairs = 32;    // pairs per work item (2 MFMA column groups of 16)
 constexpr int kQXcds = 8;      // workgroups are dispatched round robin over the 8 XCDs
-constexpr int kQBStride = 272; // LDS bytes per pair row of a term stage (256 + 16: spreads banks)
 
 // ---- activation rows -> terms ---------------------------------------------------------------
 // One wave per (row, 256-element super-block): lane l holds elements 4l .. 4l+3.
@@ -89,7 +88,7 @@ __global__ __launch_bounds__(64) void k_sh_gate(const float* __restrict__ x, int
 }
 
 // ---- grouped GEMM ---------------------------------------------------------------------------
-struct Q4Args {
+struct GQ4Args {
   ExpertLoc w0;              // gate (GATEUP) or down
   ExpertLoc w1;              // up (GATEUP)
   const float* b0;           // gate bias [E][M] or null (GATEUP)
@@ -110,20 +109,28 @@ struct Q4Args {
 
 // Work item: (expert e, row tile, 32-pair tile); 4 waves of 16 rows each (gate/up: waves 0-1 gate,
 // 2-3 up, the same 32 rows; down: 64 rows). Per 256-element super-block of K:
-//   A: lane (i, g) loads the 4 x 8 bytes of its row's quants that hold elements [8g, 8g+8) of
-//      every sub-block (low nibbles: even sub-blocks, high: odd), one super-block ahead;
-//      lanes g = 0 load the rows' 16-byte headers, decoded into LDS (d, dmin*m_j, sc_j).
+//   A: the wave's 16 rows x 144 bytes as 16-byte pieces (3 loads per lane, each covering about
+//      seven rows' whole super-blocks), one super-block ahead in registers, then written to the
+//      wave's LDS slice; lanes g = 0 decode their row's 16-byte header from it (d, dmin*m_j, sc_j)
+//      and lane (i, g) reads the 8 bytes of row i that hold elements [8g, 8g+8) of a sub-block
+//      pair (low nibbles: even sub-blocks, high: odd).
 //   B: the pairs' two term rows (32 x 2 x 256 bytes), scales and sub-block sums, staged in LDS by
-//      all 256 threads (one super-block ahead in registers, double-buffered LDS).
-// D layout of the MFMA: lane (i, g) holds rows 4g .. 4g+3 of the wave's tile, pair column i.
+//      all 256 threads (one super-block ahead in registers, double-buffered LDS) in MFMA operand
+//      order: the 8 bytes that lane l takes for (term, pair group, sub-block j) sit in slot
+//      l ^ 2j of a 512-byte block, so every LDS read of a wave is 64 consecutive 8-byte slots
+//      and the staging writes of one pair's 16 chunks spread over 8 bank pairs.
+//   min term: sum_j (dmin*m_j)[row] * X_j[pair] is a [16 x 8] x [8 x 16] f32 product per pair
+//      group, two v_mfma_f32_16x16x4_f32 per super-block instead of 8 FMAs per lane and sub-block.
+// D layout of the MFMAs: lane (i, g) holds rows 4g .. 4g+3 of the wave's tile, pair column i.
 template <bool GATEUP>
-__global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
-  __shared__ __align__(16) uint8_t bst[2][2][kQPairs * kQBStride];  // [buf][term][pair][256]
-  __shared__ float bsx[2][kQPairs * 8];                            // sub-block sums
-  __shared__ float bss[2][kQPairs];                                // term scales
-  __shared__ __align__(16) int hsc[4][8][16];                      // [wave][sub-block][row] sc_j
-  __shared__ __align__(16) float hm[4][8][16];                     // dmin*m_j
-  __shared__ __align__(16) float hd[4][16];                        // d
+__global__ __launch_bounds__(256, 3) void k_grouped_q4k(GQ4Args a) {
+  __shared__ __align__(16) uint8_t bst[2][2 * 2 * 8 * 512];  // [buf][term][pair group][sub-block][64 slots x 8 B]
+  __shared__ float bsx[2][2 * 2 * 64];                       // [buf][pair group][j / 4][lane]: sub-block sums
+  __shared__ float bss[2][kQPairs];                          // term scales
+  __shared__ __align__(16) int hsc[4][8][16];                // [wave][sub-block][row] sc_j
+  __shared__ float hm[4][2 * 64];                            // [wave][j / 4][lane]: dmin*m_j of row lane & 15
+  __shared__ __align__(16) float hd[4][16];                  // d
+  __shared__ __align__(16) uint8_t ast[4][16 * 144];         // [wave][row][super-block bytes]
   __shared__ float pw[kQPairs];                                    // routing weights (GATEUP)
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -161,12 +168,21 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
   const int wrow0 = rt * kRows + (GATEUP ? (wave & 1) : wave) * 16;
   const bool tile_in = wrow0 < a.M;  // uniform
   const uint8_t* W = expert_at(m ? a.w1 : a.w0, e);
-  const uint8_t* arow = W + (uint64_t)min(wrow0 + i, a.M - 1) * rb;  // this lane's A row
+  // A pieces of this lane: slot it*64 + lane < 144 = (row slot / 9, 16-byte piece slot % 9)
+  const uint8_t* asrc[3];
+  int adst[3];
+#pragma unroll
+  for (int it = 0; it < 3; ++it) {
+    const int sl = min(it * 64 + lane, 143);
+    asrc[it] = W + (uint64_t)min(wrow0 + sl / 9, a.M - 1) * rb + (sl % 9) * 16;
+    adst[it] = (sl / 9) * 144 + (sl % 9) * 16;
+  }
   if (GATEUP && tid < kQPairs) pw[tid] = a.pair_w ? a.pair_w[p0 + min(tid, np - 1)] : 1.f;
 
-  // B pieces of this thread: piece j*256 + tid = (term, pair, 16-byte chunk)
+  // B pieces of this thread: piece j*256 + tid = (term, pair, 16-byte chunk); the chunk holds
+  // elements [8 g0, 8 g0 + 16) of sub-block ch / 2, g0 = 2 (ch & 1): two operand slots
   const int8_t* bsrc[4];
-  int bdst[4];
+  int bdst0[4], bdst1[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int pc = j * 256 + tid;
@@ -174,8 +190,13 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
     const int p = p0 + min(pr, np - 1);
     const int row = a.pair_tok ? a.pair_tok[p] : p;
     bsrc[j] = (term ? a.t1 : a.t0) + (size_t)row * a.K + ch * 16;
-    bdst[j] = term * (kQPairs * kQBStride) + pr * kQBStride + ch * 16;
+    const int sbj = ch >> 1, g0 = 2 * (ch & 1), ii = pr & 15;
+    const int blk = ((term * 2 + (pr >> 4)) * 8 + sbj) * 512;
+    bdst0[j] = blk + ((16 * g0 + ii) ^ (2 * sbj)) * 8;
+    bdst1[j] = blk + ((16 * (g0 + 1) + ii) ^ (2 * sbj)) * 8;
   }
+  // this thread's sub-block sum (pair tid / 8, sub-block tid % 8) in B operand order
+  const int xdst = (((tid >> 3) >> 4) * 2 + ((tid & 7) >> 2)) * 64 + 16 * (tid & 3) + ((tid >> 3) & 15);
   const int xrow = [&] {  // pair of this thread's sub-block sum (tid = pair * 8 + sub-block)
     const int p = p0 + min(tid >> 3, np - 1);
     return a.pair_tok ? a.pair_tok[p] : p;
@@ -197,28 +218,36 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
   };
   auto store_b = [&](const BRegs& br, int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<i32x4*>(&bst[buf][0][0] + bdst[j]) = br.v[j];
-    bsx[buf][tid] = br.x;
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<uint64_t*>(&bst[buf][0] + bdst0[j]) =
+          ((uint64_t)(uint32_t)br.v[j][1] << 32) | (uint32_t)br.v[j][0];
+      *reinterpret_cast<uint64_t*>(&bst[buf][0] + bdst1[j]) =
+          ((uint64_t)(uint32_t)br.v[j][3] << 32) | (uint32_t)br.v[j][2];
+    }
+    bsx[buf][xdst] = br.x;
     if (tid < kQPairs) bss[buf][tid] = br.s;
   };
   struct ARegs {
-    uint32_t q[8];  // 4 x 8 bytes: elements [8g, 8g+8) of sub-block pairs 0..3
-    i32x4 hdr;      // lanes g == 0: the row's header
+    i32x4 v[3];
   };
   auto load_a = [&](int sbk, ARegs& ar) {
-    const uint8_t* sp = arow + (size_t)sbk * 144;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint64_t u = *(const __attribute__((address_space(1))) uint64_t*)(sp + 16 + 32 * p + 8 * g);
-      ar.q[2 * p] = (uint32_t)u, ar.q[2 * p + 1] = (uint32_t)(u >> 32);
-    }
-    if (g == 0) ar.hdr = *(const __attribute__((address_space(1))) i32x4*)sp;
+    for (int it = 0; it < 3; ++it)
+      if (it < 2 || lane < 16)
+        ar.v[it] = *(const __attribute__((address_space(1))) i32x4*)(asrc[it] + (size_t)sbk * 144);
   };
-  // header of row i (lanes g == 0) -> LDS: d, dmin*m_j (the reference's f32 products), sc_j
-  auto decode_hdr = [&](const ARegs& ar) {
+  auto store_a = [&](const ARegs& ar) {  // the wave's slice: its reads of the last super-block are done
+#pragma unroll
+    for (int it = 0; it < 3; ++it)
+      if (it < 2 || lane < 16) *reinterpret_cast<i32x4*>(&ast[wave][adst[it]]) = ar.v[it];
+  };
+  // header of row i (lanes g == 0, from the wave's slice) -> LDS: d, dmin*m_j (the reference's f32
+  // products), sc_j
+  auto decode_hdr = [&]() {
     if (g == 0) {
-      const uint32_t dd = (uint32_t)ar.hdr[0];
-      const uint32_t s3[3] = {(uint32_t)ar.hdr[1], (uint32_t)ar.hdr[2], (uint32_t)ar.hdr[3]};
+      const i32x4 hdr = *reinterpret_cast<const i32x4*>(&ast[wave][i * 144]);
+      const uint32_t dd = (uint32_t)hdr[0];
+      const uint32_t s3[3] = {(uint32_t)hdr[1], (uint32_t)hdr[2], (uint32_t)hdr[3]};
       const float d = h2f(dd & 0xFFFFu), dmin = h2f(dd >> 16);
       hd[wave][i] = d;
 #pragma unroll
@@ -226,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
         uint32_t sc, mm;
         q4k_scale_min((uint32_t)j, s3, sc, mm);
         hsc[wave][j][i] = (int)sc;
-        hm[wave][j][i] = dmin * (float)mm;
+        hm[wave][(j >> 2) * 64 + 16 * (j & 3) + i] = dmin * (float)mm;
       }
     }
   };
@@ -234,51 +263,58 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
   f32x4 acc[2];
   acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
   BRegs bR;
-  ARegs aC, aN;
+  ARegs aR;
   load_b(0, bR);
-  load_a(0, aC);
+  load_a(0, aR);
   for (int sbk = 0; sbk < nsb; ++sbk) {
     const int buf = sbk & 1;
     store_b(bR, buf);  // buffer buf was last read in super-block sbk-2, before the last barrier
-    decode_hdr(aC);    // this wave's header slots were last read before the last barrier
-    __syncthreads();   // the stage of super-block sbk and the headers are in LDS
+    store_a(aR);
+    decode_hdr();      // this wave's header slots were last read before the last barrier
+    __syncthreads();   // the stages of super-block sbk and the headers are in LDS
     if (sbk + 1 < nsb) {
       load_b(sbk + 1, bR);
-      load_a(sbk + 1, aN);
+      load_a(sbk + 1, aR);
     }
     if (tile_in) {
-      const uint8_t* b0 = &bst[buf][0][0];
-      const uint8_t* b1 = &bst[buf][1][0];
+      const uint8_t* bb = &bst[buf][0];
       int I0[2][4], I1[2][4];
-      float Mn[2][4];
 #pragma unroll
       for (int pg = 0; pg < 2; ++pg)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) I0[pg][r] = I1[pg][r] = 0, Mn[pg][r] = 0.f;
+        for (int r = 0; r < 4; ++r) I0[pg][r] = I1[pg][r] = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         // A: elements [8g, 8g+8) of sub-block j of row i as int8 (low nibbles: even j)
-        const uint32_t lo = aC.q[2 * (j >> 1)], hi = aC.q[2 * (j >> 1) + 1];
+        const uint64_t qb = *reinterpret_cast<const uint64_t*>(&ast[wave][i * 144 + 16 + 32 * (j >> 1) + 8 * g]);
+        const uint32_t lo = (uint32_t)qb, hi = (uint32_t)(qb >> 32);
         const uint32_t sh = (j & 1) * 4;
         const long av = (long)(((uint64_t)((hi >> sh) & 0x0F0F0F0Fu) << 32) | ((lo >> sh) & 0x0F0F0F0Fu));
         const i32x4v scv = *reinterpret_cast<const i32x4v*>(&hsc[wave][j][4 * g]);
-        const f32x4 mv = *reinterpret_cast<const f32x4*>(&hm[wave][j][4 * g]);
+        const int slot = (lane ^ (2 * j)) * 8;
 #pragma unroll
         for (int pg = 0; pg < 2; ++pg) {
-          const int pr = pg * 16 + i;
-          const long bv0 = *reinterpret_cast<const long*>(b0 + pr * kQBStride + 32 * j + 8 * g);
-          const long bv1 = *reinterpret_cast<const long*>(b1 + pr * kQBStride + 32 * j + 8 * g);
+          const long bv0 = *reinterpret_cast<const long*>(bb + ((0 * 2 + pg) * 8 + j) * 512 + slot);
+          const long bv1 = *reinterpret_cast<const long*>(bb + ((1 * 2 + pg) * 8 + j) * 512 + slot);
           const i32x4v z = {0, 0, 0, 0};
           const i32x4v d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv0, z, 0, 0, 0);
           const i32x4v d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv1, z, 0, 0, 0);
-          const float xs = bsx[buf][pr * 8 + j];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             I0[pg][r] += __mul24(scv[r], d0[r]);
             I1[pg][r] += __mul24(scv[r], d1[r]);
-            Mn[pg][r] = __builtin_fmaf(mv[r], xs, Mn[pg][r]);
           }
         }
+      }
+      // min term: [16 rows x 8 sub-blocks] x [8 sub-blocks x 16 pairs] per pair group
+      f32x4 Mn[2];
+#pragma unroll
+      for (int pg = 0; pg < 2; ++pg) {
+        Mn[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          Mn[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(hm[wave][c * 64 + lane], bsx[buf][(pg * 2 + c) * 64 + lane],
+                                                        Mn[pg], 0, 0, 0);
       }
       const f32x4 dv = *reinterpret_cast<const f32x4*>(&hd[wave][4 * g]);
 #pragma unroll
@@ -291,11 +327,10 @@ __global__ __launch_bounds__(256, 2) void k_grouped_q4k(Q4Args a) {
         }
       }
     }
-    aC = aN;
   }
   if (GATEUP) {
     __syncthreads();  // every wave is done with the stages: reuse them for the gate/up tiles
-    float* ep = reinterpret_cast<float*>(&bst[0][0][0]);  // [mat][32 rows][32 pairs]
+    float* ep = reinterpret_cast<float*>(&bst[0][0]);  // [mat][32 rows][32 pairs]
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg)
 #pragma unroll
@@ -415,7 +450,7 @@ hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x
   if ((e = launch_group(K, idx, w, P, k, E, pair_tok, pair_w, pair_of, exp_off, tile_off)) != hipSuccess) return e;
   if ((e = split(K, x, T, (uint32_t)H, xt)) != hipSuccess) return e;
   const int max_tiles = (P + kQPairs - 1) / kQPairs + E;
-  Q4Args a{};
+  GQ4Args a{};
   a.w0 = expert_loc(L.d.gate), a.w1 = expert_loc(L.d.up), a.b0 = L.d.gate_bias, a.b1 = L.d.up_bias;
   a.t0 = xt.t0, a.t1 = xt.t1, a.bs = xt.s, a.bx = xt.x;
   a.pair_tok = pair_tok, a.pair_w = pair_w, a.exp_off = exp_off, a.tile_off = tile_off;
@@ -426,7 +461,7 @@ hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if ((e = split(K, h, (uint64_t)P, (uint32_t)I, ht)) != hipSuccess) return e;
-  Q4Args d{};
+  GQ4Args d{};
   d.w0 = expert_loc(L.d.down);
   d.t0 = ht.t0, d.t1 = ht.t1, d.bs = ht.s, d.bx = ht.x;
   d.exp_off = exp_off, d.tile_off = tile_off, d.out = o, d.M = H, d.K = I, d.E = E;
@@ -443,7 +478,7 @@ hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x
     osh = reinterpret_cast<float*>(b + p.osh);
     sig = reinterpret_cast<float*>(b + p.sig);
     const int tiles = ((int)T + kQPairs - 1) / kQPairs;
-    Q4Args s{};
+    GQ4Args s{};
     s.w0 = expert_loc(L.d.sh_gate), s.w1 = expert_loc(L.d.sh_up);
     s.t0 = xt.t0, s.t1 = xt.t1, s.bs = xt.s, s.bx = xt.x;
     s.single_p = (int)T, s.out = hsh, s.M = Ish, s.K = H, s.E = 1, s.act = MR_ACT_SILU;
@@ -453,7 +488,7 @@ hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if ((e = split(K, hsh, T, (uint32_t)Ish, hst)) != hipSuccess) return e;
-    Q4Args sd{};
+    GQ4Args sd{};
     sd.w0 = expert_loc(L.d.sh_down);
     sd.t0 = hst.t0, sd.t1 = hst.t1, sd.bs = hst.s, sd.bx = hst.x;
     sd.single_p = (int)T, sd.out = osh, sd.M = H, sd.K = Ish, sd.E = 1;

@@ -172,6 +172,9 @@ hipError_t launch_rms_norm(const Launch& K, const float* h, const float* w, floa
                            float* out);
 hipError_t launch_residual_add(const Launch& K, const float* h, const float* m, uint64_t n, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
+// Measurement probes (mr_probe.hip).
+hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t* sink);
+hipError_t launch_probe_empty(const Launch& K, uint32_t n_wg);
 // With `device` current: this device's address of the static scratch array (looked up once
 // per device).
 hipError_t static_scratch_init(int device, void** out);

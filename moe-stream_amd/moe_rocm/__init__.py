@@ -91,6 +91,8 @@ _SIGS = {
     "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_moe_forward_batched_residual": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _f32, _vp]),
+    "mr_probe_read": (C.c_int, [_vp, _vp, _u64, _u32, _vp]),
+    "mr_probe_empty": (C.c_int, [_vp, _u32]),
     "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "mr_gguf_close": (None, [_vp]),
@@ -220,6 +222,12 @@ class Context:
         g = _vp()
         self.check(_lib.mr_graph_end(self.h, C.byref(g)))
         return Graph(self, g.value)
+
+    def probe_read(self, src, nbytes: int, n_workgroups: int, sink) -> None:
+        self.check(_lib.mr_probe_read(self.h, _ptr(src), nbytes, n_workgroups, _ptr(sink)))
+
+    def probe_empty(self, n_workgroups: int) -> None:
+        self.check(_lib.mr_probe_empty(self.h, n_workgroups))
 
     def synth_blocks(self, ggml_type: int, dst: "DeviceBuffer", n_blocks: int, seed: int,
                      offset: int = 0) -> None:

@@ -1,6 +1,8 @@
 """Build libmoe_rocm.so (the C-ABI library) for gfx950 with hipcc, in-tree.
 
-Usage: python -m moe_rocm.build   (from moe-stream_amd/), or moe_rocm.build.build().
+Usage: python moe-stream_amd/moe_rocm/build.py [--trace], or moe_rocm.build.build().
+--trace builds the same library with the fused decode kernel's phase timestamps compiled in
+(MR_FUSED_TRACE; read by `bench.py --trace`) as moe_rocm/trace/libmoe_rocm.so.
 """
 from __future__ import annotations
 
@@ -26,6 +28,7 @@ HIP_FLAGS = [
 
 
 EXTRA_FLAGS = os.environ.get("MOE_ROCM_EXTRA_FLAGS", "").split()
+TRACE_LIB = PKG_DIR / "trace" / "libmoe_rocm.so"
 
 
 def sources() -> list[Path]:
@@ -43,11 +46,16 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False, out: Path | None = None, obj_dir: Path | None = None) -> Path:
-    global OBJ_DIR
+def build(verbose: bool = False, out: Path | None = None, obj_dir: Path | None = None, trace: bool = False) -> Path:
+    global OBJ_DIR, EXTRA_FLAGS
+    if trace:
+        EXTRA_FLAGS = [*EXTRA_FLAGS, "-DMR_FUSED_TRACE"]
+        obj_dir = obj_dir or OBJ_DIR / "trace"
+        out = out or TRACE_LIB
     if obj_dir is not None:
         OBJ_DIR = obj_dir
     lib_path = out or LIB_PATH
+    lib_path.parent.mkdir(parents=True, exist_ok=True)
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
@@ -64,5 +72,5 @@ def build(verbose: bool = False, out: Path | None = None, obj_dir: Path | None =
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, trace="--trace" in sys.argv[1:])
     sys.exit(0)

@@ -278,4 +278,9 @@ extern "C" {
 
     // ---- synthetic inputs
     pub fn mr_synth_blocks(ctx: *mut mr_ctx, ggml_type: c_int, dst: *mut c_void, n_blocks: u64, seed: u64) -> c_int;
+
+    // ---- measurement probes
+    pub fn mr_probe_read(ctx: *mut mr_ctx, src: *const c_void, nbytes: u64, n_workgroups: u32, sink: *mut u32)
+        -> c_int;
+    pub fn mr_probe_empty(ctx: *mut mr_ctx, n_workgroups: u32) -> c_int;
 }

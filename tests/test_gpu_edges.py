@@ -96,3 +96,22 @@ def test_nan_logits_rank_below_every_number(gpu_ctx, name, kernel):
         gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
         dl.close()
         dx.free(), dy.free()
+
+
+def test_probe_read_reads_every_byte(gpu_ctx):
+    """mr_probe_read (the plain-stream ceiling of bench.py --probe) folds every 32-bit word of
+    the buffer into the per-workgroup sinks: their XOR is the XOR of the whole buffer, for a
+    grid that divides the buffer evenly and one that leaves a ragged tail."""
+    rng = np.random.default_rng(11)
+    data = rng.integers(0, 2**32, size=(1 << 20) // 4 + 4 * 37, dtype=np.uint32)
+    want = np.bitwise_xor.reduce(data)
+    d = gpu_ctx.to_device(data)
+    for n_wg in (64, 548):
+        sink = gpu_ctx.alloc(n_wg * 4)
+        gpu_ctx.probe_read(d, data.nbytes, n_wg, sink)
+        got = np.bitwise_xor.reduce(sink.download(np.uint32))
+        assert got == want, n_wg
+        sink.free()
+    gpu_ctx.probe_empty(576)
+    gpu_ctx.sync()
+    d.free()
