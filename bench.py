@@ -430,8 +430,11 @@ def bench_batched(a, ctx, M, W, spec):
         ach = flops[dom] / (avg_ms * 1e-3) / 1e12
         q4 = dom.startswith("grouped_q4k")
         peak = MFMA_INT8_PEAK_TOPS if q4 else MFMA_FP8_PEAK_TFLOPS
+        tr = measured_traffic(a.config) if a.config == 5 and not a.batched else None
+        traffic = int(tr["bytes_per_launch"]) if tr and tr.get("kernel") == dom else None
         roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": peak,
-                "unit": "TOP/s" if q4 else "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None,
+                "unit": "TOP/s" if q4 else "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic,
+                "traffic_source": "profiles/traffic.json (rocprofv3 --pmc)" if traffic else None,
                 "flops_per_launch": flops[dom], "avg_launch_us": round(avg_ms * 1e3, 2),
                 "note": ("GEMM ops of the layer; the 2-term int8 activation split issues 2x this MFMA work"
                          if q4 else "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this "

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(64) void k_sh_gate(const float* __restrict__ x, int
   const int t = blockIdx.x, lane = threadIdx.x;
   float z = 0.f;
   if (gi)
-    for (int c = lane; c < H; c += 64) z = __builtin_fmaf(x[(size_t)t * H + c], gi[c], z);
+#pragma unroll 8
+    for (int c = lane; c < H; c += 64) z = __builtin_fmaf(x[(size_t)t * H + c], gi[c], z);  // loads issued ahead
   z = wave_sum(z);
   if (lane == 0) sig[t] = gi ? sigmoidf_(z) : 1.0f;
 }
