@@ -176,7 +176,7 @@ def probes() -> None:
 
 
 def trace_decode(a) -> None:
-    """Phase timestamps of one fused MXFP4 decode launch (device clock, 100 MHz, read at each
+    """Phase timestamps of one fused decode launch (device clock, 100 MHz, read at each
     role's phase boundaries by thread 0 of every workgroup; the first workgroup start is 0).
     The launch is layer 5 of the seventh token of the bench's layer ring, enqueued eagerly after
     six tokens through every layer, so its router rows were prefetched by layer 4 as in the timed
@@ -200,7 +200,11 @@ def trace_decode(a) -> None:
         stack.enqueue_token(t)
     li = 5 % len(specs)
     s0 = specs[li]
-    R, ND, NG = (s0.n_experts + 3) // 4, (s0.hidden + 15) // 16, s0.top_k * (s0.inter // 32)
+    if s0.mxfp4:
+        R, ND, NG = (s0.n_experts + 3) // 4, (s0.hidden + 15) // 16, s0.top_k * (s0.inter // 32)
+    else:  # Q4_K: the shared expert is one more router row and one more gate/up slot
+        has_sh = 1 if s0.sh_inter else 0
+        R, ND, NG = (s0.n_experts + has_sh + 3) // 4, s0.hidden // 16, (s0.top_k + has_sh) * (s0.inter // 16)
     buf = ctx.zeros((1024 * 32,), dtype=np.uint64)
     def launch(l):
         if a.residual:
@@ -234,6 +238,27 @@ def trace_decode(a) -> None:
                  "weights_prepared": q(us[role == "down", 2]), "gateup_count_seen": q(us[role == "down", 3]),
                  "image_in_lds": q(us[role == "down", 4]), "exit": q(us[role == "down", 5])},
     }
+    # routing points of the consumer workgroups (slots 8-15, thread 0): poll start, every logit
+    # seen, keys formed, top-k selected, state kept
+    for rname in ("gateup", "down"):
+        raw = tr[:grid][role == rname]
+        sel = us[role == rname]
+        for slot, name in ((8, "route_poll_start"), (9, "route_logits_seen"), (11, "route_keys"),
+                           (13, "route_topk_done"), (15, "route_state_kept")):
+            ok = raw[:, slot] != 0
+            if ok.any():
+                phases[rname][name] = q(sel[ok, slot])
+        if raw[:, 10].any():
+            phases[rname]["route_polls"] = q(raw[:, 10].astype(np.float64))
+    # per-wave points (slots 16-23, where the kernel records them): gate/up dot products done
+    # (16 + wave); down dot products done (16 + wave) and combine done (20 + wave)
+    for rname in ("gateup", "down"):
+        sel = us[role == rname]
+        raw = tr[:grid][role == rname]
+        for slot, name in ((16, "wave_dots_done"), (20, "wave_combine_done")):
+            v = np.concatenate([sel[raw[:, slot + w] != 0, slot + w] for w in range(4)])
+            if v.size:
+                phases[rname][name] = q(v)
     cu = [(b % 8, int(tr[b, 7])) for b in range(grid)]  # (XCD, hardware CU id); workgroup b runs on XCD b mod 8
     by_cu = {}
     for b in range(grid):

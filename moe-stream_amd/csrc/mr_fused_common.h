@@ -467,7 +467,10 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   RTRACE(0);
   const int nj = (rc.E + 63) >> 6;  // values per lane (wave-uniform)
   // Poll the flagged logit words until every entry (experts and extras) carries this
-  // launch's flag; the values come with the flags, in the same loads.
+  // launch's flag; the values come with the flags, in the same loads. One poll at a time:
+  // a poll is a round trip to the device-coherent level (about a microsecond), yet more
+  // polls in flight (2-4, spaced over that round trip) delay the logits' own stores and
+  // lose 3-35% (the publish lines are shared by every consumer workgroup).
   const uint64_t* lw = logit_copy(rc.fs, rc.n_logits, (int)(blockIdx.x % kLogitCopies));
   const uint32_t flag = seq + 1u;
   const int ex = lane < (int)rc.n_logits - rc.E ? rc.E + lane : -1;  // an extra entry of this lane
@@ -485,7 +488,12 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
       }
     }
     if (ex >= 0) ok = ok && (uint32_t)(ld64_sc1(lw + ex) >> 32) == flag;
-    if (__ballot(!ok) == 0ull) break;
+    if (__ballot(!ok) == 0ull) {
+#ifdef MR_FUSED_TRACE
+      if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 32 + 10] = it;  // polls before the logits were seen
+#endif
+      break;
+    }
     if (it >= rc.spin_limit) return false;
     __builtin_amdgcn_s_sleep(SLEEP);
   }

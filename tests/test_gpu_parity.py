@@ -98,7 +98,25 @@ TINY_Q4P = W.LayerSpec(204, 0, W.GGML_Q4_K, 512, 256, 12, 3, 0, W.ACT_SILU, Fals
 # top-10 of 20 experts: the 16-slot combine of the grouped path and a ragged 16-expert router tile
 TINY_MXK = W.LayerSpec(205, 0, W.GGML_MXFP4, 512, 384, 20, 10, W.ROUTE_NORM_TOPK, W.ACT_SWIGLU_OAI,
                        True, True)
+# Q4_K shapes past the fixed-shape fused instantiations (I/256 <= 3, H <= 2048, slots per down
+# wave within its registers): they run the streaming instantiation, units passed through the
+# registers in rounds; top-16 plus a shared expert is the widest routing the fused kernels take.
+WIDE_Q4 = {
+    "q4k-H4096": W.LayerSpec(206, 0, W.GGML_Q4_K, 4096, 512, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, False),
+    "q4k-H3072-I768": W.LayerSpec(207, 0, W.GGML_Q4_K, 3072, 768, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU, False, False),
+    "q4k-I1536-k8": W.LayerSpec(208, 0, W.GGML_Q4_K, 1024, 1536, 16, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
+                                False),
+    "q4k-I1024-k7-shared": W.LayerSpec(209, 0, W.GGML_Q4_K, 2048, 1024, 32, 7, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                       False, False, sh_inter=1024),
+    "q4k-k16-shared": W.LayerSpec(215, 0, W.GGML_Q4_K, 512, 256, 64, 16, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
+                                  False, sh_inter=256),
+    # a Qwen3-235B-A22B-shaped layer (H 4096, I 1536, 128 experts, top-8): two row tiles per gate/up
+    # workgroup keep its grid resident
+    "q4k-235b-shape": W.LayerSpec(216, 0, W.GGML_Q4_K, 4096, 1536, 128, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
+                                  False),
+}
 SPECS = {
+    **WIDE_Q4,
     "tiny-mxfp4": TINY_MX,
     "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
@@ -356,7 +374,7 @@ def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
-         "C4-coder-next-layer0", *C4_RANGE]
+         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4]
 
 
 @pytest.mark.parametrize("name", FUSED)
