@@ -23,13 +23,16 @@
 // Three groups of workgroups share one grid:
 //   [0, R)        router: one expert logit per wave; publishes it as a flagged
 //                 64-bit word (logit bits, launch number + 1).
-//   [R, R+ND)     down: 16 output rows; wave w takes routed slot w (top_k <= 4).
-//                 Its down weights are loaded into registers before the gate/up
-//                 results exist, so their HBM traffic overlaps the gate/up phase.
-//   [R+ND, grid)  gate/up: 32 rows of one routed slot, both projections; 4
-//                 waves = (gate, up) x 2 row tiles, each over the full K. The x
-//                 split is built in LDS while the router runs. Epilogue: bias,
-//                 SwiGLU, x routing weight, split into the down B image.
+//   [R, R+ND)     down: 16 output rows; wave w takes slots w, w+4, ... (routed
+//                 slots, then the shared expert). The down weights of its first
+//                 slot are loaded into registers before the gate/up results exist,
+//                 so their HBM traffic overlaps the gate/up phase; a later slot's
+//                 are loaded once the previous slot is done (top_k > 4 only).
+//   [R+ND, grid)  gate/up: 32 rows of one slot, both projections; 4 waves =
+//                 (gate, up) x 2 row tiles, each over the full K. The x split is
+//                 built in LDS while the router runs. Epilogue: bias, SwiGLU (SiLU
+//                 for the shared expert), x routing weight (the sigmoid gate for
+//                 the shared expert, layer.rs:1935-1951), split into the down B image.
 // Workgroups are dispatched in index order; fused_supported keeps R + ND below
 // the CU count and the whole grid within 3 workgroups per CU (159 VGPRs, about
 // 50 KB LDS each), so every workgroup is resident from the start and no wait
@@ -67,14 +70,20 @@ struct FusedArgs {
   float* y;
   uint32_t* fs;   // this layer's sync block
   uint32_t* err;  // context error word (read and cleared by mr_sync)
-  uint8_t* dimg;  // [k][nbI][kImgBytes] down B image
-  uint32_t* dsc;  // [k][nbI] 4 e8m0 bytes (one per term)
-  int H, I, E, k;
+  const uint8_t* sh_gate;  // shared expert matrices (one expert, MXFP4) or null
+  const uint8_t* sh_up;
+  const uint8_t* sh_down;
+  const float* sh_gate_inp;
+  uint8_t* dimg;  // [ktot][nbI][kImgBytes] down B image
+  uint32_t* dsc;  // [ktot][nbI] 4 e8m0 bytes (one per term)
+  float* dpart;   // [ktot][H] down rows of each slot (more than four slots: combined by the last slot group)
+  int H, I, E, k, ktot, has_sh;
   uint32_t flags;
   int act;
   float alpha, limit;
   int R, NG, ND;
-  int NS;  // down row groups split into two 8-row workgroups (CU balance)
+  int NS;        // down row groups split into two 8-row workgroups (CU balance; at most four slots)
+  int NDR, nsl;  // row groups and slot groups of the down role (ND = NDR * nsl)
   uint32_t spin_limit;
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
@@ -88,15 +97,17 @@ struct FusedArgs {
 // past the row end (clamped to the last block, or zero windows) meet an all-zero B operand,
 // so any finite operand serves them: their codes are finite whatever the bytes, but their
 // scale byte is set to 127, since a misaligned byte could be 0xFF (NaN, and NaN * 0 = NaN).
-// Done while the workgroup waits for the gate/up results.
-__device__ __forceinline__ void prep_rows(RawBlk (&rw)[kSteps], uint32_t sh, int nb, int g) {
+// Done while the workgroup waits for the gate/up results. N steps from step j0 (the whole
+// row, or a part of it where the rows are loaded after the wait).
+template <int N = kSteps>
+__device__ __forceinline__ void prep_rows(RawBlk (&rw)[N], uint32_t sh, int nb, int g, int j0 = 0) {
   const uint32_t s0 = (sh + (uint32_t)g) & 3u;  // scale byte position
   const uint32_t t = s0 + 1u;                   // code bytes start
   const bool hi = t == 4u;
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
+  for (int j = 0; j < N; ++j) {
     RawBlk& r = rw[j];
-    const uint32_t sa = 4 * j + g < nb ? (r.d[0] >> (8u * s0)) & 0xFFu : 127u;
+    const uint32_t sa = 4 * (j0 + j) + g < nb ? (r.d[0] >> (8u * s0)) & 0xFFu : 127u;
     const uint32_t q0 = hi ? r.d[1] : __builtin_amdgcn_alignbyte(r.d[1], r.d[0], t);
     const uint32_t q1 = hi ? r.d[2] : __builtin_amdgcn_alignbyte(r.d[2], r.d[1], t);
     const uint32_t q2 = hi ? r.d[3] : __builtin_amdgcn_alignbyte(r.d[3], r.d[2], t);
@@ -110,11 +121,13 @@ __device__ __forceinline__ void prep_rows(RawBlk (&rw)[kSteps], uint32_t sh, int
 // 4..15 repeat columns 0..3; only columns 0..3 are summed) at fixed offsets from one base:
 // block 4j + (g>>1) of step j is at j*512, the block two later at j*512 + 256, and the
 // scale byte of block 4j+g at j*16 -- no address arithmetic per step.
-__device__ __forceinline__ f32x4 mfma_chain_p(const RawBlk (&rw)[kSteps], const uint8_t* img,
-                                              const uint32_t* sc, int i, int g) {
-  const uint8_t* bb = img + (g >> 1) * kImgBytes + (i & 3) * 32 + 16 * (g & 1);
-  const uint8_t* sbp = reinterpret_cast<const uint8_t*>(sc) + g * 4 + (i & 3);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+// N steps from step j0 accumulate into acc (even steps) and acc1 (odd steps), so a row taken
+// in parts gives the same sums as in one pass.
+template <int N>
+__device__ __forceinline__ void mfma_chain_part(const RawBlk (&rw)[N], const uint8_t* img, const uint32_t* sc,
+                                                int i, int g, int j0, f32x4& acc, f32x4& acc1) {
+  const uint8_t* bb = img + (g >> 1) * kImgBytes + (i & 3) * 32 + 16 * (g & 1) + j0 * 4 * kImgBytes;
+  const uint8_t* sbp = reinterpret_cast<const uint8_t*>(sc) + g * 4 + (i & 3) + j0 * 16;
   // B operands (and scale bytes) of steps j+1 and j+2 are in flight while step j multiplies
   constexpr int kAhead = 2;
   i32x4 b0[kAhead + 1], b1[kAhead + 1];
@@ -126,9 +139,9 @@ __device__ __forceinline__ f32x4 mfma_chain_p(const RawBlk (&rw)[kSteps], const 
     sb[j] = sbp[j * 16];
   }
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
+  for (int j = 0; j < N; ++j) {
     const int cur = j % (kAhead + 1);
-    if (j + kAhead < kSteps) {
+    if (j + kAhead < N) {
       const int nx = (j + kAhead) % (kAhead + 1);
       b0[nx] = *reinterpret_cast<const i32x4*>(bb + (j + kAhead) * 4 * kImgBytes);
       b1[nx] = *reinterpret_cast<const i32x4*>(bb + (j + kAhead) * 4 * kImgBytes + 2 * kImgBytes);
@@ -138,24 +151,29 @@ __device__ __forceinline__ f32x4 mfma_chain_p(const RawBlk (&rw)[kSteps], const 
     const i32x8 B = {b0[cur][0], b0[cur][1], b0[cur][2], b0[cur][3], b1[cur][0], b1[cur][1], b1[cur][2], b1[cur][3]};
     const RawBlk& r = rw[j];
     const i32x8 A = {(int)r.d[0], (int)r.d[1], (int)r.d[2], (int)r.d[3], 0, 0, 0, 0};
-    if (j & 1)
+    if ((j0 + j) & 1)
       acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc1, 4, 0, 0, (int)r.d[4], 0, sb[cur]);
     else
       acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc, 4, 0, 0, (int)r.d[4], 0, sb[cur]);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+__device__ __forceinline__ f32x4 mfma_chain_p(const RawBlk (&rw)[kSteps], const uint8_t* img,
+                                              const uint32_t* sc, int i, int g) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  mfma_chain_part<kSteps>(rw, img, sc, i, g, 0, acc, acc1);
   return f32x4{acc[0] + acc1[0], acc[1] + acc1[1], acc[2] + acc1[2], acc[3] + acc1[3]};
 }
 
 // A operands (raw windows) of one 16-row tile, all K steps (S is wave-uniform).
 // Blocks past the row end (last step, lane groups g beyond nb) load the row's
 // last block instead: their B operand is all zero, so they add exactly 0.
-__device__ __forceinline__ void issue_rows(const uint8_t* W, int S, int nb, int g,
-                                           RawBlk (&rw)[kSteps]) {
+template <int N = kSteps>
+__device__ __forceinline__ void issue_rows(const uint8_t* W, int S, int nb, int g, RawBlk (&rw)[N], int j0 = 0) {
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
-    if (j < S)
-      raw_load(W + (size_t)min(4 * j + g, nb - 1) * 17, rw[j]);
+  for (int j = 0; j < N; ++j) {
+    if (j0 + j < S)
+      raw_load(W + (size_t)min(4 * (j0 + j) + g, nb - 1) * 17, rw[j]);
     else
       raw_zero(rw[j]);
   }
@@ -274,15 +292,19 @@ __device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, i
 // ---- the kernel ----------------------------------------------------------------------------
 // NORM: the input is rms_norm(x) and the residual x is added to y (mr_moe_forward_residual);
 // a separate instantiation, so the plain decode path compiles without that code.
-template <bool NORM>
+// GEN: a shared expert or more than four slots (top_k + shared). With more than four, the
+// down role has one workgroup per row group and group of four slots (a.nsl groups), each
+// wave one slot as in the plain case, and the last group of a row group to finish combines
+// every slot from the partials buffer. !GEN (top_k <= 4, no shared expert) compiles none of it.
+template <bool NORM, bool GEN>
 __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   extern __shared__ __align__(16) uint8_t lds_dyn[];
   uint8_t* lds_img = lds_dyn;
   uint32_t* lds_sc = reinterpret_cast<uint32_t*>(lds_dyn + a.lds_img_bytes);
-  __shared__ float lds_part[2 * 2 * 2 * 16];
+  __shared__ float lds_part[2 * 2 * 2 * 16];  // gate/up: [gate, up][tile][16]; down: [wave][16]
   __shared__ float lds_act[32];
   __shared__ int sel_i[16];
-  __shared__ float sel_w[16];
+  __shared__ float sel_w[17];  // [k]: weight of the shared expert
   __shared__ int sel_o[16];
   __shared__ uint32_t sel_k[16];
   __shared__ uint32_t route_tmp[128];  // routing: compacted candidates
@@ -295,23 +317,25 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   const int nbH = a.H >> 5, nbI = a.I >> 5;
   TRACE(0);
   const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
-  const RouteCfg rc{a.fs, (uint32_t)a.E, a.E, a.k, a.flags, a.spin_limit, a.trace};
+  const int has_sh = GEN ? a.has_sh : 0, ktot = GEN ? a.ktot : a.k;
+  const RouteCfg rc{a.fs, (uint32_t)(a.E + has_sh), a.E, a.k, a.flags, a.spin_limit, a.trace};
   if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
     __builtin_amdgcn_s_setprio(2);  // the logits gate every other role: router loads issue first
     const int e = bid * 4 + wave;
-    if (e < a.E) {
-      const float* w = a.router_w + (size_t)e * a.H;
+    if (e < a.E + has_sh) {
+      // experts, then the shared expert's gate row (x . w_gi, its sigmoid gate)
+      const float* w = e < a.E ? a.router_w + (size_t)e * a.H : a.sh_gate_inp;
       // bias and mask are loaded with the rows, not after the reduction (an HBM round trip)
-      const float rbias = a.router_b ? a.router_b[e] : 0.f;
-      const float rmask = a.mask ? a.mask[e] : 0.f;
+      const float rbias = (e < a.E && a.router_b) ? a.router_b[e] : 0.f;
+      const float rmask = (e < a.E && a.mask) ? a.mask[e] : 0.f;
       f32x4 xv[kRouterVec], wv[kRouterVec];  // every load issued before the first use
 #pragma unroll
       for (int j = 0; j < kRouterVec; ++j) {
         const int c = (lane + 64 * j) * 4;
-        const bool in = c < a.H;
+        const bool in = c < a.H && w != nullptr;
         xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
         wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
       }
@@ -333,9 +357,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
       }
       acc = wave_sum(acc);  // the same bits in every lane (butterfly of commutative adds)
-      if (a.router_b) acc = acc + rbias;
-      if (a.mask) acc = acc + rmask;
-      put_logit(a.fs, (uint32_t)a.E, e, seq, acc);
+      if (e < a.E) {
+        if (a.router_b) acc = acc + rbias;
+        if (a.mask) acc = acc + rmask;
+      }
+      put_logit(a.fs, (uint32_t)(a.E + has_sh), e, seq, acc);
     }
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, lds_dyn);
@@ -402,14 +428,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     if (ok_flag && gid < a.NG) {  // one unit per workgroup
       const int unit = gid;
       const int slot = unit / nrp, pair = unit % nrp;
-      const int e = sel_i[slot];
+      const bool sh = slot >= a.k;  // the shared expert
+      const int e = sh ? 0 : sel_i[slot];
       const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
       const int S = (nbH + 3) >> 2;
       const uint64_t rb = (uint64_t)nbH * 17;
-      const uint8_t* W = expert_at(mat ? a.up : a.gate, e) + (uint64_t)(pair * 32 + tile * 16) * rb;
-      // the epilogue's biases (wave 0, lanes < 32), loaded before the weight stream
-      float gbias = 0.f, ubias = 0.f;
-      if (wave == 0 && lane < 32) {
+      const uint8_t* W = (sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e)) +
+                         (uint64_t)(pair * 32 + tile * 16) * rb;
+      // the epilogue's biases (wave 0, lanes < 32) and shared gate logit, loaded before the stream
+      float gbias = 0.f, ubias = 0.f, zsh = 0.f;
+      if (wave == 0 && has_sh && lane == 0) zsh = get_logit(a.fs, (uint32_t)(a.E + has_sh), a.E);
+      if (wave == 0 && lane < 32 && !sh) {
         const size_t bi = (size_t)e * a.I + pair * 32 + lane;
         if (a.gate_b) gbias = a.gate_b[bi];
         if (a.up_b) ubias = a.up_b[bi];
@@ -421,6 +450,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
                                   });
       XTRACE(4 + wave);  // per wave: chain done
       TRACE(3);
+      if (wave == 0 && has_sh && lane == 0) sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(zsh) : 1.f;
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -433,10 +463,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           const int t2 = lane >> 4, r16 = lane & 15;
           float gv = lds_part[(0 * 2 + t2) * 16 + r16];
           float uv = lds_part[(1 * 2 + t2) * 16 + r16];
-          if (a.gate_b) gv = gv + gbias;
-          if (a.up_b) uv = uv + ubias;
-          const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-          lds_act[lane] = h * sel_w[slot];  // written by this wave's route_finish
+          if (!sh && a.gate_b) gv = gv + gbias;
+          if (!sh && a.up_b) uv = uv + ubias;
+          const float h = (!sh && a.act == MR_ACT_SWIGLU_OAI) ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
+          lds_act[lane] = h * sel_w[slot];  // written by this wave's route_finish (the shared gate above)
         }
         __builtin_amdgcn_wave_barrier();
         if (lane < 8) {  // split the 32 values: one 32-element block of the down input
@@ -461,8 +491,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     // Row group q of 16 output rows. The first NS groups are split: rows 0-7 here, rows
     // 8-15 in a workgroup after the gate/up range (half 2). A half's idle lanes read the
     // row of their partner lane (i ^ 8): the same addresses, so no extra HBM bytes.
+    // Row group q, slot group sg (slots 4 sg + wave; 0 unless GEN with more than four slots).
     const int tail = bid - (a.R + a.ND + a.NG);
-    const int q = tail >= 0 ? tail : bid - a.R;
+    const int dq = tail >= 0 ? tail : bid - a.R;
+    const int q = GEN ? dq % a.NDR : dq, sg = GEN ? dq / a.NDR : 0;
     const int half = tail >= 0 ? 2 : (q < a.NS ? 1 : 0);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once the prefetch is issued
@@ -479,11 +511,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const int S = (nbI + 3) >> 2;
       const int row = q * 16 + (half == 0 ? i : (half == 2 ? 8 : 0) + (i & 7));
       const uint64_t rb = (uint64_t)nbI * 17;
-      f32x4 d = {0.f, 0.f, 0.f, 0.f};
       RawBlk rd[kSteps];
-      int slot = wave;
-      const uint8_t* D = expert_at(a.down, sel_i[slot < a.k ? slot : 0]) + (uint64_t)row * rb;
-      if (slot < a.k) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
+      const int slot = sg * 4 + wave;  // this wave's slot (routed, then the shared expert)
+      const int sl = min(slot, ktot - 1);
+      const uint8_t* D = (sl >= a.k ? a.sh_down : expert_at(a.down, sel_i[sl])) + (uint64_t)row * rb;
+      if (slot < ktot) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
       int so[4] = {0, 0, 0, 0};
@@ -496,8 +528,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       float ybias = 0.f;
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
-      const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u;
-      if (slot < a.k) prep_rows(rd, sh, nbI, g);  // waits for the weights: they land long before gate/up ends
+      if (slot < ktot)  // waits for the weights: they land long before gate/up ends
+        prep_rows(rd, (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u, nbI, g);
       TRACE(2);
       if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 64>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
         ok_flag = 0, fail(a.err);
@@ -506,15 +538,15 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       if (ok_flag) {
         uint8_t* wimg = lds_img + (size_t)wave * kImgVec * 1024;  // this wave's slot image
         uint32_t* wsc = lds_sc + wave * 128;
-        if (slot < a.k) {  // one slot per wave (top_k <= 4)
+        if (slot < ktot) {
           {  // slot image -> LDS with direct global->LDS loads (no VGPRs in flight)
             const uint8_t* src = a.dimg + (size_t)slot * nbI * kImgBytes;
             const int n16 = nbI * kImgBytes / 16;
 #pragma unroll
-            for (int j = 0; j < kImgVec; ++j) {
-              if (64 * j < n16) {
-                const int idx = min(lane + 64 * j, n16 - 1);
-                __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, wimg + 1024 * j, 16, 0, 16 /* sc1 */);
+            for (int jj = 0; jj < kImgVec; ++jj) {
+              if (64 * jj < n16) {
+                const int idx = min(lane + 64 * jj, n16 - 1);
+                __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, wimg + 1024 * jj, 16, 0, 16 /* sc1 */);
               }
             }
             const uint32_t sc0 = ld_sc1(a.dsc + slot * nbI + min(lane, nbI - 1));
@@ -532,25 +564,50 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           }
           TRACE(4);
           XTRACE(wave);  // per wave: image in LDS
-          d = mfma_chain_p(rd, wimg, wsc, i, g);
+          const f32x4 d = mfma_chain_p(rd, wimg, wsc, i, g);
           XTRACE(4 + wave);  // per wave: chain done
-        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float s = sum4(d[r]);
-          if (i == 0) lds_part[wave * 16 + 4 * g + r] = s;
+          for (int r = 0; r < 4; ++r) {
+            const float cs = sum4(d[r]);
+            if (i == 0) lds_part[wave * 16 + 4 * g + r] = cs;
+          }
         }
         __syncthreads();
-        if (tid < 16 && (half == 0 || (tid >> 3) == half - 1)) {
-          const int rr = q * 16 + tid;
-          float yv = 0.f;  // slots in ascending expert order (layer.rs:1092-1106)
+        if (!GEN || a.nsl == 1) {
+          if (tid < 16 && (half == 0 || (tid >> 3) == half - 1)) {
+            const int rr = q * 16 + tid;
+            float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
 #pragma unroll
-          for (int p = 0; p < 4; ++p)
-            if (p < a.k) yv = yv + lds_part[so[p] + tid];
-          yv = yv + ybias;
-          if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
-          if (rr < a.H) a.y[rr] = yv;
-          XTRACE(8);
+            for (int p = 0; p < 4; ++p)
+              if (p < a.k) yv = yv + lds_part[so[p] + tid];
+            yv = yv + ybias;
+            if (has_sh) yv = yv + lds_part[a.k * 16 + tid];  // shared expert after the routed sum
+            if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
+            if (rr < a.H) a.y[rr] = yv;
+            XTRACE(8);
+          }
+        } else {
+          // this slot group's rows -> the partials buffer; the row group's last slot group to
+          // finish (a counter per row group, nothing waits) combines every slot
+          if (tid < 64 && sg * 4 + (tid >> 4) < ktot) {
+            st_sc1(reinterpret_cast<uint32_t*>(a.dpart) + (size_t)(sg * 4 + (tid >> 4)) * a.H + q * 16 + (tid & 15),
+                   __float_as_uint(lds_part[tid]));
+            vm_drain();  // partials complete before the count that announces them
+          }
+          __syncthreads();
+          if (tid == 0)
+            ok_flag = add_sc1(a.fs + FS_DN + q, 1u) + 1u == (seq + 1u) * (uint32_t)a.nsl ? 2 : 1;
+          __syncthreads();
+          if (ok_flag == 2 && tid < 16) {
+            const int rr = q * 16 + tid;
+            const uint32_t* part = reinterpret_cast<const uint32_t*>(a.dpart);
+            float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
+            for (int p = 0; p < a.k; ++p) yv = yv + __uint_as_float(ld_sc1(part + (size_t)sel_o[p] * a.H + rr));
+            yv = yv + ybias;
+            if (has_sh) yv = yv + __uint_as_float(ld_sc1(part + (size_t)a.k * a.H + rr));  // shared expert last
+            if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
+            a.y[rr] = yv;
+          }
         }
       }
     }
@@ -569,10 +626,23 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 // Shapes the fused kernel runs; others take the VALU path.
 uint64_t fused_layer_sync_bytes(const mr_layer& L) { return layer_sync_words(L.E + (L.d.sh_gate ? 1u : 0u)) * 4; }
 
+// More than four slots (top_k > 4, or a shared expert with top_k = 4): one down workgroup
+// per row group and group of four slots. A shared expert or more than four slots: the GEN
+// instantiation.
+static bool fused_multi(const mr_layer& L) { return L.d.top_k + (L.d.sh_gate ? 1u : 0u) > 4u; }
+static bool fused_gen(const mr_layer& L) { return L.d.sh_gate != nullptr || fused_multi(L); }
+
 bool fused_supported(const mr_layer& L, int n_cu) {
-  if (L.type != MR_GGML_MXFP4 || L.d.sh_gate || L.d.top_k > 4) return false;
-  const uint64_t R = (L.E + 3) / 4, ND = (L.H + 15) / 16, NG = (uint64_t)L.d.top_k * (L.I / 32);
-  if (R + ND >= (uint64_t)n_cu || R + ND + NG > 3ull * n_cu) return false;  // one dispatch round
+  if (L.type != MR_GGML_MXFP4 || L.d.top_k > 16) return false;
+  const uint64_t has_sh = L.d.sh_gate ? 1u : 0u;
+  if (has_sh && (L.d.sh_gate->type != MR_GGML_MXFP4 || L.d.sh_up->type != MR_GGML_MXFP4 ||
+                 L.d.sh_down->type != MR_GGML_MXFP4 || L.Ish != L.I))
+    return false;  // a shared expert: MXFP4 like the routed ones, and as wide
+  if (L.E + has_sh > (uint64_t)kMaxLogits) return false;
+  const uint64_t ktot = L.d.top_k + has_sh, nsl = (ktot + 3) / 4;
+  const uint64_t R = (L.E + has_sh + 3) / 4, ND = (L.H + 15) / 16 * nsl, NG = ktot * (L.I / 32);
+  if (!fused_multi(L) && R + ND >= (uint64_t)n_cu) return false;  // routers and down groups in one dispatch round
+  if (R + ND + NG > 3ull * n_cu) return false;
   if (R + ND + NG > (uint64_t)kMaxGrid) return false;  // the split groups are added only where they fit
   const uint64_t nbH = L.H / 32, nbI = L.I / 32;
   if ((nbH + 3) / 4 > (uint64_t)kSteps || (nbI + 3) / 4 > (uint64_t)kSteps) return false;
@@ -592,16 +662,19 @@ extern "C" void mr_debug_fused_trace(void* dev_buf) { g_fused_trace = (unsigned 
 // down group carry three units; splitting those down groups in halves, the second half
 // in a third-round slot on a CU with two units, caps every CU at 2.5 units.
 struct FusedGrid {
-  int R, ND, NG, NS;
+  int R, ND, NG, NS, NDR, nsl;
   int total() const { return R + ND + NG + NS; }
 };
 static FusedGrid fused_grid(const mr_layer& L, int n_cu) {
   FusedGrid g;
-  g.R = (int)((L.E + 3) / 4);
-  g.NG = (int)(L.d.top_k * (L.I / 32));
-  g.ND = (int)((L.H + 15) / 16);
+  const uint32_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + has_sh;
+  g.R = (int)((L.E + has_sh + 3) / 4);
+  g.NG = (int)(ktot * (L.I / 32));
+  g.NDR = (int)((L.H + 15) / 16);
+  g.nsl = (int)((ktot + 3) / 4);
+  g.ND = g.NDR * g.nsl;
   const int grid0 = g.R + g.ND + g.NG;
-  g.NS = std::max(0, std::min({g.ND + g.NG - 2 * n_cu, g.ND, 3 * n_cu - grid0, kMaxGrid - grid0}));
+  g.NS = fused_multi(L) ? 0 : std::max(0, std::min({g.ND + g.NG - 2 * n_cu, g.ND, 3 * n_cu - grid0, kMaxGrid - grid0}));
   return g;
 }
 // Dynamic LDS of a launch: the gate/up role's x image (nbH blocks), the down role's four
@@ -616,11 +689,16 @@ static uint64_t fused_lds_bytes(const mr_layer& L) {
 // Every workgroup of a launch must be resident at once (workgroups wait on each other):
 // the occupancy the runtime reports for this kernel's registers and LDS, on an otherwise
 // idle device, times the CU count must cover the grid (both instantiations).
+template <bool NORM>
+static const void* fused_kernel(const mr_layer& L) {
+  return fused_gen(L) ? reinterpret_cast<const void*>(k_fused_mxfp4<NORM, true>)
+                      : reinterpret_cast<const void*>(k_fused_mxfp4<NORM, false>);
+}
 bool fused_resident(const mr_layer& L, int n_cu) {
   const size_t lds = fused_lds_bytes(L);
   int b0 = 0, b1 = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, k_fused_mxfp4<false>, 256, lds) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, k_fused_mxfp4<true>, 256, lds) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, fused_kernel<false>(L), 256, lds) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, fused_kernel<true>(L), 256, lds) != hipSuccess)
     return false;
   return (int64_t)std::min(b0, b1) * n_cu >= fused_grid(L, n_cu).total();
 }
@@ -635,14 +713,22 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.gate = expert_loc(L.d.gate), a.up = expert_loc(L.d.up), a.down = expert_loc(L.d.down);
   a.gate_b = L.d.gate_bias, a.up_b = L.d.up_bias, a.down_b = L.d.down_bias;
   a.router_w = L.d.router_w, a.router_b = L.d.router_b, a.mask = L.d.dummy_mask;
+  a.has_sh = L.d.sh_gate ? 1 : 0;
+  if (a.has_sh) {
+    a.sh_gate = L.d.sh_gate->base + L.d.sh_gate->h_offsets[0];
+    a.sh_up = L.d.sh_up->base + L.d.sh_up->h_offsets[0];
+    a.sh_down = L.d.sh_down->base + L.d.sh_down->h_offsets[0];
+    a.sh_gate_inp = L.d.sh_gate_inp;
+  }
   a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
-  const uint64_t nbH = L.H / 32, nbI = L.I / 32, k = L.d.top_k;
+  const uint64_t nbH = L.H / 32, nbI = L.I / 32, k = L.d.top_k, ktot = k + (uint64_t)a.has_sh;
   a.dimg = img_base;
-  a.dsc = reinterpret_cast<uint32_t*>(img_base + k * nbI * kImgBytes);
-  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k;
+  a.dsc = reinterpret_cast<uint32_t*>(img_base + ktot * nbI * kImgBytes);
+  a.dpart = reinterpret_cast<float*>(img_base + ((ktot * nbI * (kImgBytes + 4) + 255) & ~(uint64_t)255));
+  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k, a.ktot = (int)ktot;
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   const FusedGrid fg = fused_grid(L, n_cu);
-  a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS;
+  a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl;
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
@@ -650,10 +736,10 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   const size_t lds = fused_lds_bytes(L);
   (void)nbH;
   ProfScope ps(K, "fused_layer");
-  if (nr.w)
-    hipLaunchKernelGGL(k_fused_mxfp4<true>, dim3(fg.total()), dim3(256), lds, K.s, a);
-  else
-    hipLaunchKernelGGL(k_fused_mxfp4<false>, dim3(fg.total()), dim3(256), lds, K.s, a);
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchKernel(nr.w ? fused_kernel<true>(L) : fused_kernel<false>(L), dim3(fg.total()), dim3(256),
+                                       args, lds, K.s);
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 

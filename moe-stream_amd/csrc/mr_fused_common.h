@@ -32,7 +32,8 @@ static_assert(kLogitCopies >= 1 && kLogitCopies <= 64, "one copy per lane of the
 enum : int {
   FS_GU = 0,                                   // [kCopies] counter: gate/up units finished
   FS_WGSEQ = FS_GU + kCopies * kCopyStride,    // [grid] launches completed, one word per workgroup
-  FS_LOGITS = FS_WGSEQ + kMaxGrid              // [kLogitCopies][n_logits] (logit bits, launch flag)
+  FS_DN = FS_WGSEQ + kMaxGrid,                 // [row groups] down slot groups finished (MXFP4, > 4 slots)
+  FS_LOGITS = FS_DN + kMaxGrid                 // [kLogitCopies][n_logits] (logit bits, launch flag)
                                                // word pairs: E experts, then extras
 };
 // The block's size for n_logits published logits (logit_copy's stride times the copies).

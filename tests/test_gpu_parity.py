@@ -115,8 +115,21 @@ WIDE_Q4 = {
     "q4k-235b-shape": W.LayerSpec(216, 0, W.GGML_Q4_K, 4096, 1536, 128, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
                                   False),
 }
+# MXFP4 layers with more than four slots (one down workgroup per row group and group of four
+# slots, the last to finish combining) and with an MXFP4 shared expert
+WIDE_MX = {
+    "mxfp4-k3-shared": W.LayerSpec(217, 0, W.GGML_MXFP4, 512, 384, 16, 3, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                                   W.ACT_SWIGLU_OAI, True, True, sh_inter=384, sh_type=W.GGML_MXFP4),
+    "mxfp4-k4-shared": W.LayerSpec(218, 0, W.GGML_MXFP4, 1024, 512, 32, 4, W.ROUTE_NORM_TOPK, W.ACT_SWIGLU_OAI,
+                                   True, True, sh_inter=512, sh_type=W.GGML_MXFP4),
+    "mxfp4-k8": W.LayerSpec(219, 0, W.GGML_MXFP4, 1024, 1024, 32, 8, W.ROUTE_SOFTMAX_AFTER_TOPK, W.ACT_SWIGLU_OAI,
+                            True, True),
+    "mxfp4-k16-shared": W.LayerSpec(220, 0, W.GGML_MXFP4, 512, 256, 32, 16, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
+                                    False, sh_inter=256, sh_type=W.GGML_MXFP4),
+}
 SPECS = {
     **WIDE_Q4,
+    **WIDE_MX,
     "tiny-mxfp4": TINY_MX,
     "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
@@ -374,7 +387,7 @@ def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
-         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4]
+         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4, *WIDE_MX, "tiny-mxfp4-k10"]
 
 
 @pytest.mark.parametrize("name", FUSED)
