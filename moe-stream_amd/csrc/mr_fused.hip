@@ -296,7 +296,7 @@ __device__ __forceinline__ f32x4 stream_chain_v(const uint8_t* W, uint32_t rb, i
 // down role has one workgroup per row group and group of four slots (a.nsl groups), each
 // wave one slot as in the plain case, and the last group of a row group to finish combines
 // every slot from the partials buffer. !GEN (top_k <= 4, no shared expert) compiles none of it.
-template <bool NORM, bool GEN>
+template <bool NORM, bool GEN, bool QWEN>
 __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   extern __shared__ __align__(16) uint8_t lds_dyn[];
   uint8_t* lds_img = lds_dyn;
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     TRACE(1);
     if (tid == 0) ok_flag = 1;
     RouteState rs;  // wave 0: the selection, finished (weights, order) once its stream is issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
+    if (wave == 0 && !route_select<MR_ROUTE_SLEEP, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     XTRACE(wave);  // per wave: at the routing barrier
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     // the routing wave runs at the gate/up waves' priority while it selects (its weight
     // prefetch, issued after, stays below the gate/up streams)
     if (wave == 0) __builtin_amdgcn_s_setprio(1);
-    if (wave == 0 && !route_select<MR_ROUTE_SLEEP_DOWN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
+    if (wave == 0 && !route_select<MR_ROUTE_SLEEP_DOWN, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
       if (lane == 0) ok_flag = 0, fail(a.err);
     }
     if (wave == 0) __builtin_amdgcn_s_setprio(0);
@@ -691,8 +691,13 @@ static uint64_t fused_lds_bytes(const mr_layer& L) {
 // idle device, times the CU count must cover the grid (both instantiations).
 template <bool NORM>
 static const void* fused_kernel(const mr_layer& L) {
-  return fused_gen(L) ? reinterpret_cast<const void*>(k_fused_mxfp4<NORM, true>)
-                      : reinterpret_cast<const void*>(k_fused_mxfp4<NORM, false>);
+  // the near-tie check of probability ranking only where the layer ranks probabilities
+  const bool qwen = !(L.d.route_flags & MR_ROUTE_SOFTMAX_AFTER_TOPK);
+  if (fused_gen(L))
+    return qwen ? reinterpret_cast<const void*>(k_fused_mxfp4<NORM, true, true>)
+                : reinterpret_cast<const void*>(k_fused_mxfp4<NORM, true, false>);
+  return qwen ? reinterpret_cast<const void*>(k_fused_mxfp4<NORM, false, true>)
+              : reinterpret_cast<const void*>(k_fused_mxfp4<NORM, false, false>);
 }
 bool fused_resident(const mr_layer& L, int n_cu) {
   const size_t lds = fused_lds_bytes(L);

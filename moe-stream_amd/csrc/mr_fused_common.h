@@ -344,6 +344,76 @@ constexpr int kRouteVals = 8;  // experts per lane in routing: E <= 512
 #define MR_ROUTE_SLEEP_DOWN 100  // down workgroups: their weights are needed only after gate/up
 #endif
 
+// ---- Qwen-mode ranking: probabilities, ties to the lower index --------------------------
+// The standard mode ranks p_i = expf(l_i - max) / sum in f32 (sum in expert order; layer.rs:
+// 2371-2394) with a stable sort whose comparator calls unordered pairs equal. exp and the
+// division are monotonic, so ranking by logit selects the same set unless
+//  - the k-th selected logit lk and the largest logit below it lb are so close that their
+//    probabilities can round to one value: the f32 difference l - max is exact to 2^-24
+//    |l - max|, expf and the division round once each, so lk - lb > 2^-20 (1 + max - lb) keeps
+//    p(lk) > p(lb) while p(lk) is a normal number, which max - lk <= 80 ensures (expf(-80) / 512
+//    > 2^-126); below that, probabilities lose precision or flush to 0 and tie;
+//  - a probability is NaN: a NaN logit, a +inf maximum (inf - inf) or a row of -inf make the
+//    sum, hence every probability, NaN; every comparison is then "equal" and the stable sort
+//    keeps expert order: experts 0..k-1 with NaN weights.
+// prob_exact_needed tells those rows apart; they are ranked again on the probabilities.
+// key: this lane's key columns (valid logits have keys >= 2, NaN 1, absent 0), T the k-th
+// largest key. The common answer costs a wave max and one compare pass.
+__device__ __forceinline__ bool prob_exact_needed(const uint32_t (&key)[kRouteVals], uint32_t T) {
+  uint32_t mk = 0u;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) mk = max(mk, key[j]);
+  const float lk = key_value(T), m = key_value(wave_max_u(mk)), d = m - lk;
+  // lb >= lk - tau with tau = 2^-20 (1 + m - lb) <= 2^-20 (1 + m - lk) (1 + 2^-19): any key in
+  // [key(lk - tau), T) is a near tie
+  const uint32_t lo = order_key(lk - 0x1p-20f * (1.f + d) * (1.f + 0x1p-19f));
+  // Branch-free (bitwise, not short-circuit: the compiler would turn every || into a branch
+  // on the exec mask): NaN or infinite ends, or p(lk) below the normal range; then per key a
+  // near tie or a NaN (which makes every probability NaN; absent keys, 0, lie below lo).
+  uint32_t hit = !(d <= 80.f) ? 1u : 0u;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j)
+    hit |= ((key[j] >= lo ? 1u : 0u) & (key[j] < T ? 1u : 0u)) | (key[j] == 1u ? 1u : 0u);
+  return __ballot(hit != 0u) != 0ull;
+}
+// Order keys of the probabilities as the reference computes them: expf of the f32 difference
+// (correctly rounded: computed in double), the sum in expert order (each term read from its
+// lane in turn, so every lane adds the same sequence), IEEE division. NaN probabilities get key
+// 1 (equal to each other), absent experts (past E) key 0. Returns whether they are NaN. Registers only, and rolled where it can be: the path is rare, and it must not
+// weigh on the caller's registers or LDS.
+__device__ __forceinline__ bool prob_keys(const float (&v)[kRouteVals], int E, uint32_t (&key)[kRouteVals]) {
+  const int lane = threadIdx.x & 63;
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j)
+    if (lane + 64 * j < E) m = fmaxf(m, v[j]);
+  m = wave_max_f(m);
+  float p[kRouteVals], s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    p[j] = lane + 64 * j < E ? (float)exp((double)(v[j] - m)) : 0.f;
+    const int n = min(64, E - 64 * j);  // experts of column j
+#pragma unroll 1
+    for (int l = 0; l < n; ++l) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j]), l));
+  }
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    const float q = p[j] / s;
+    key[j] = lane + 64 * j < E ? (q == q ? order_key(q + 0.f) : 1u) : 0u;
+  }
+  return !(s == s);  // the sum (the same in every lane) is NaN exactly when every probability is
+}
+// The value of lane-held entry e (lane e & 63, column e >> 6), in every lane.
+__device__ __forceinline__ float entry_value(const float (&v)[kRouteVals], int e) {
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    const float t = __shfl(v[j], e & 63);
+    if ((e >> 6) == j) r = t;
+  }
+  return r;
+}
+
 // Lanes below this one in a 64-bit wave mask.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
@@ -390,10 +460,11 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[kRouteVals], i
 // The selected set: keys above T, then of the keys equal to T the lowest expert indices.
 // Expert indices idx[j] ascend with j, then with the lane (e = lane + 64*j, or a list
 // compacted in that order). Slot = rank of the expert index among the selected, so slots
-// run in ascending expert order. sel_i/sel_k[slot] get the expert and its key.
+// run in ascending expert order. sel_i/sel_k[slot] get the expert and its key. Returns T,
+// the k-th largest key.
 template <int NJ>
-__device__ __forceinline__ void topk_slots(const uint32_t (&key)[kRouteVals], const int (&idx)[kRouteVals], int k,
-                                           int* sel_i, uint32_t* sel_k) {
+__device__ __forceinline__ uint32_t topk_slots(const uint32_t (&key)[kRouteVals], const int (&idx)[kRouteVals], int k,
+                                               int* sel_i, uint32_t* sel_k) {
   const uint32_t T = kth_key<NJ>(key, k);
   int above = 0;
 #pragma unroll
@@ -412,14 +483,15 @@ __device__ __forceinline__ void topk_slots(const uint32_t (&key)[kRouteVals], co
     }
     before += __popcll(sm);
   }
+  return T;
 }
 
 // Many columns (E > 128): the k-th largest lane maximum H bounds the threshold from
 // below (k lanes hold a key >= H), so only keys >= H can be selected. When those fit one
-// column they are compacted in ascending expert order through LDS (tmp: 128 words) and
+// column they are compacted in ascending expert order through LDS (tmp: 128 of its words) and
 // selected there; otherwise all columns are searched.
-__device__ __forceinline__ void topk_slots_wide(const uint32_t (&key)[kRouteVals], int k, int* sel_i, uint32_t* sel_k,
-                                                uint32_t* tmp) {
+__device__ __forceinline__ uint32_t topk_slots_wide(const uint32_t (&key)[kRouteVals], int k, int* sel_i,
+                                                    uint32_t* sel_k, uint32_t* tmp) {
   const int lane = threadIdx.x & 63;
   uint32_t hm[kRouteVals], hk = 0u;
 #pragma unroll
@@ -438,20 +510,17 @@ __device__ __forceinline__ void topk_slots_wide(const uint32_t (&key)[kRouteVals
   int idx[kRouteVals];
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
-  if (before > 64) {
-    topk_slots<kRouteVals>(key, idx, k, sel_i, sel_k);
-    return;
-  }
+  if (before > 64) return topk_slots<kRouteVals>(key, idx, k, sel_i, sel_k);
   lds_drain();
   __builtin_amdgcn_wave_barrier();
   uint32_t ck[kRouteVals];
   ck[0] = lane < before ? tmp[lane] : 0u;
   idx[0] = lane < before ? (int)tmp[64 + lane] : 0;
-  topk_slots<1>(ck, idx, k, sel_i, sel_k);
+  return topk_slots<1>(ck, idx, k, sel_i, sel_k);
 }
 
 // Wave 0 of a consumer workgroup (all 64 lanes): wait until every logit of this
-// launch is published, then select the top-k (largest first, ties to the lower
+// launch is published, then select the top-k (tmp: kRouteVals * 64 words of LDS scratch) (largest first, ties to the lower
 // index; top_k_routing layer.rs:2346-2403). Expert e = lane + 64*j is value j of
 // a lane. Slots are numbered in ascending expert index, the combine order of
 // layer.rs:1092-1106; slot r's expert goes to sel_i[r] (LDS) and, for route_finish,
@@ -461,7 +530,65 @@ struct RouteState {
   uint32_t my_key;
   int my_e;
 };
-template <int SLEEP = MR_ROUTE_SLEEP>
+// The selection by key (topk_slots for one or two key columns, else topk_slots_wide) into
+// sel_i/sel_k; returns the k-th largest key.
+__device__ __forceinline__ uint32_t select_keys(const uint32_t (&key)[kRouteVals], int nj, int k, int* sel_i,
+                                                uint32_t* sel_k, uint32_t* tmp) {
+  const int lane = threadIdx.x & 63;
+  int idx[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
+  const uint32_t T = nj <= 1   ? topk_slots<1>(key, idx, k, sel_i, sel_k)
+                     : nj <= 2 ? topk_slots<2>(key, idx, k, sel_i, sel_k)
+                               : topk_slots_wide(key, k, sel_i, sel_k, tmp);
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+  return T;
+}
+
+// The selection redone on probability keys (pkey: order keys of p, absent 0): k rounds of a wave
+// argmax on (key, complemented index), then the k experts put in ascending expert order into
+// sel_i/sel_k (sel_k: their logit keys, which route_finish weighs by; the NaN key 1 when the
+// probabilities are NaN (pnan), so the weights come out NaN as the reference's do). Small and
+// slow: such rows are rare, and this code must not weigh on the routing's registers.
+__device__ __forceinline__ void prob_select(const uint32_t (&pkey)[kRouteVals], const float (&v)[kRouteVals], int E,
+                                            int k, bool pnan, int* sel_i, uint32_t* sel_k) {
+  const int lane = threadIdx.x & 63;
+  bool live[kRouteVals];
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) live[j] = lane + 64 * j < E;
+  int mine = 0;  // lane r: the r-th ranked expert
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0ull;
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j) {
+      const uint64_t key = ((uint64_t)pkey[j] << 32) | (0xFFFFFFFFu - (uint32_t)(lane + 64 * j));
+      if (live[j]) best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
+#pragma unroll
+    for (int j = 0; j < kRouteVals; ++j)
+      if (bi == lane + 64 * j) live[j] = false;
+    if (lane == r) mine = bi;
+  }
+  // slot = rank of the expert index among the selected
+  int slot = 0;
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) {
+    const int o = __shfl(mine, r);
+    slot += (lane < k && o < mine) ? 1 : 0;
+  }
+  const float ls = entry_value(v, mine);
+  if (lane < k) sel_i[slot] = mine, sel_k[slot] = (ls == ls && !pnan) ? order_key(ls + 0.f) : 1u;
+  lds_drain();
+  __builtin_amdgcn_wave_barrier();
+}
+
+// QWEN: compile in the near-tie check (layers whose flags lack MR_ROUTE_SOFTMAX_AFTER_TOPK rank
+// probabilities); a kernel instantiated without it ranks by logit alone.
+template <int SLEEP = MR_ROUTE_SLEEP, bool QWEN = true>
 __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, uint32_t* sel_k, uint32_t* tmp,
                                    RouteState& st) {
   const int lane = threadIdx.x & 63;
@@ -499,9 +626,9 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
     __builtin_amdgcn_s_sleep(SLEEP);
   }
   RTRACE(1);
-  // Ranking: largest logit first. The reference ranks softmax probabilities in Qwen
-  // mode; exp is monotonic, so the order differs only where two logits round to the
-  // same probability (a tie by value, which the tests treat as ambiguous).
+  // Ranking: largest logit first, then in Qwen mode, where two logits at the selection
+  // boundary could round to one probability, or that hold NaN probabilities, again on the
+  // probabilities (prob_exact_needed).
   // Keys: + 0.f makes -0.0 and +0.0 share a key; a NaN takes key 1, below every number
   // (-inf is 0x007FFFFF) and above the absent entries past E (key 0), the order of k_topk.
   uint32_t key[kRouteVals];
@@ -509,17 +636,11 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   for (int j = 0; j < kRouteVals; ++j)
     key[j] = (lane + 64 * j < rc.E) ? (v[j] == v[j] ? order_key(v[j] + 0.f) : 1u) : 0u;
   RTRACE(3);
-  int idx[kRouteVals];
-#pragma unroll
-  for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
-  if (nj <= 1)
-    topk_slots<1>(key, idx, rc.k, sel_i, sel_k);
-  else if (nj <= 2)
-    topk_slots<2>(key, idx, rc.k, sel_i, sel_k);
-  else
-    topk_slots_wide(key, rc.k, sel_i, sel_k, tmp);
-  lds_drain();
-  __builtin_amdgcn_wave_barrier();
+  const uint32_t T = select_keys(key, nj, rc.k, sel_i, sel_k, tmp);
+  if (QWEN && !(rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) && prob_exact_needed(key, T)) {
+    const bool pnan = prob_keys(v, rc.E, key);
+    prob_select(key, v, rc.E, rc.k, pnan, sel_i, sel_k);
+  }
   RTRACE(5);
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) st.v[j] = v[j];

@@ -380,9 +380,12 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       load_lanes4(a.x, a.H, hv);
       inv = rms_inv(hv, a.H, a.nr.eps);
     }
-    // x image: one 16-element group per thread of waves 1-3 (wave 0 goes straight to the
-    // logit poll, which the routing of every gate/up workgroup waits on)
-    for (int G = tid - 64; G < (a.H >> 4); G += 192) {
+    // The routing wave goes straight to the logit poll, which the routing of every gate/up
+    // workgroup waits on. It differs between the (up to four) workgroups that share a CU
+    // (workgroups b and b + 256 share one), so their polls and selections run on different SIMDs.
+    const int rw = (bid >> 8) & 3;
+    // x image: one 16-element group per thread of the other three waves
+    for (int G = wave == rw ? -1 : (wave - (wave > rw ? 1 : 0)) * 64 + lane; G < (a.H >> 4); G += 192) {
       if (G < 0) break;
       float v[16];
 #pragma unroll
@@ -401,10 +404,11 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       x_group(v, xq, xs, G);
     }
     TRACE(1);
-    if (tid == 0) ok_flag = 1;
-    RouteState rs;  // wave 0: the selection, finished (weights, order) once its loads are issued
-    if (wave == 0 && !route_select(rc, seq, sel_i, sel_k, route_tmp, rs)) {
-      if (lane == 0) ok_flag = 0, fail(a.err);
+    RouteState rs;  // the routing wave: the selection, finished (weights, order) once its loads are issued
+    if (wave == rw) {  // ok_flag written by this wave alone: it is 0 exactly when the selection failed
+      const bool routed = route_select(rc, seq, sel_i, sel_k, route_tmp, rs);
+      if (lane == 0) ok_flag = routed ? 1 : 0;
+      if (!routed && lane == 0) fail(a.err);
     }
     __syncthreads();  // selection and the x image ready
     TRACE(2);
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         // nu == 0 of the row block's first super-block) add nothing
         const uint8_t* Wl = nu > 0 ? Wr : uniform_ptr(W + (size_t)(urow * 16) * rb);
         units_issue(R, max(nu, 1), [&](int u) { return Wl + (size_t)u * 144; }, ul);
-        if (wave == 0 && t == 0) route_finish(rc, rs, sel_w, sel_o);  // routing weights while the rows load
+        if (wave == rw && t == 0) route_finish(rc, rs, sel_w, sel_o);  // routing weights while the rows load
         // the LDS operands of unit r + 1 are read before unit r's MFMAs
         UnitOps op = unit_ops(ul, (uint32_t)min(c0, nsbH - 1) * 16u, smem);
 #pragma unroll
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         }
       } else {
         if (nu > 0) units_issue(R, nu, base, ul);
-        if (wave == 0 && t == 0) route_finish(rc, rs, sel_w, sel_o);
+        if (wave == rw && t == 0) route_finish(rc, rs, sel_w, sel_o);
         if (nu > 0)
           units_process<STREAM>(R, nu, base, ul, [&](int u, const uint4& hd, const uint4& w0, const uint4& w1) {
             acc += unit_dot(hd, w0, w1, ul, (uint32_t)(c0 + u) * 16u, smem);

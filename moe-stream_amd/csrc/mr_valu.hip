@@ -137,65 +137,93 @@ hipError_t launch_router_logits(const Launch& K, const mr_layer& L, const float*
 // fused_ops.metal:131-316). One wave per token; each lane holds up to 8 of the
 // E <= 512 values. Selection = first k of a stable descending sort: the
 // largest value wins, ties go to the lower expert index.
-// Top-k of the logits v[j] of experts lane + 64 j (live[j]: e < E).
+// Top-k of the logits v[j] of experts lane + 64 j (live[j]: e < E): by logit, and in the
+// standard mode, where two logits at the selection boundary could round to one probability,
+// again by the probabilities as the reference computes them (prob_exact_needed, prob_keys);
+// rows whose probabilities are NaN then take experts 0..k-1, as the reference's stable sort does.
 __device__ void topk_vals(float (&v)[8], bool (&live)[8], int k, uint32_t flags, int32_t* out_idx,
                           float* out_w, float* sel_v /* LDS [16] */, int* sel_i /* LDS [16] */) {
+  static_assert(kRouteVals == 8, "one key column per lane value");
   const int lane = threadIdx.x & 63;
   const bool softmax_after = (flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) != 0u;
-  float mx_all = 0.f, sum_all = 0.f;
-  if (!softmax_after) {
-    // standard mode: probabilities over all experts, then select by probability
+  int E = 0;  // live[j] is e < E
+#pragma unroll
+  for (int j = 0; j < 8; ++j) E += __popcll(__ballot(live[j]));
+  // keys: + 0.f makes -0.0 and +0.0 share a key; a NaN takes key 1, below every number
+  // (-inf is 0x007FFFFF), as in the fused routing
+  uint32_t hk[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) hk[j] = live[j] ? (v[j] == v[j] ? order_key(v[j] + 0.f) : 1u) : 0u;
+  // k rounds of a wave argmax on 64-bit keys: the value's order key above the complemented
+  // expert index, so the larger value wins and, between equal values, the lower index. DPP
+  // steps inside 16-lane rows, then the four rows by readlane. Returns the k-th key.
+  auto select = [&]() {
+    bool lv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lv[j] = live[j];
+    uint32_t kth = 0u;
+    for (int r = 0; r < k; ++r) {
+      uint64_t best = 0ull;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t e = (uint32_t)(lane + 64 * j);
+        const uint64_t key = ((uint64_t)hk[j] << 32) | (0xFFFFFFFFu - e);
+        if (lv[j]) best = key > best ? key : best;
+      }
+      best = wave_max_u64(best);
+      const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
+      if ((bi & 63) == lane) lv[bi >> 6] = false;
+      if (lane == 0) sel_i[r] = bi;
+      kth = (uint32_t)(best >> 32);
+    }
+    __builtin_amdgcn_wave_barrier();
+    return kth;
+  };
+  const uint32_t kth = select();
+  if (!softmax_after && prob_exact_needed(hk, kth)) {
+    prob_keys(v, E, hk);
+    select();
+  }
+  // the selected logits
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) {
+    const float lr = entry_value(v, sel_i[r]);
+    if (lane == 0) sel_v[r] = lr;
+  }
+  __builtin_amdgcn_wave_barrier();
+  float mx_all = 0.f, sum_all = 1.f;
+  if (!softmax_after) {  // standard mode: probabilities over all experts
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       if (live[j]) m = fmaxf(m, v[j]);
     mx_all = wave_max(m);
-    float s = 0.f;
+    float sm = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (live[j]) {
-        v[j] = __expf(v[j] - mx_all);
-        s += v[j];
-      }
-    sum_all = wave_sum(s);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (live[j]) v[j] = v[j] / sum_all;
+      if (live[j]) sm += __expf(v[j] - mx_all);
+    sum_all = wave_sum(sm);
   }
-  // k rounds of a wave argmax on 64-bit keys: the value's order key above the complemented
-  // expert index, so the larger value wins and, between equal values, the lower index (a NaN
-  // ranks below every number). DPP steps inside 16-lane rows, then the four rows by readlane.
-  for (int r = 0; r < k; ++r) {
-    uint64_t best = 0ull;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t e = (uint32_t)(lane + 64 * j);
-      const uint32_t hk = v[j] == v[j] ? order_key(v[j] + 0.f) : 0u;  // + 0.f: -0.0 ties +0.0
-      const uint64_t key = ((uint64_t)hk << 32) | (0xFFFFFFFFu - e);
-      if (live[j]) best = key > best ? key : best;
-    }
-    best = wave_max_u64(best);
-    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-    if ((bi & 63) == lane) live[bi >> 6] = false;
-    if (lane == 0) sel_v[r] = key_value((uint32_t)(best >> 32)), sel_i[r] = bi;
-  }
-  __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
     if (softmax_after) {
       float m = -INFINITY;
       for (int r = 0; r < k; ++r) m = fmaxf(m, sel_v[r]);
-      float ex[16], s = 0.f;
+      float ex[16], sx = 0.f;
       for (int r = 0; r < k; ++r) {
         ex[r] = __expf(sel_v[r] - m);
-        s = s + ex[r];
+        sx = sx + ex[r];
       }
-      for (int r = 0; r < k; ++r) out_w[r] = ex[r] / s;
-    } else if (flags & MR_ROUTE_NORM_TOPK) {
-      float s = 0.f;
-      for (int r = 0; r < k; ++r) s = s + sel_v[r];
-      for (int r = 0; r < k; ++r) out_w[r] = sel_v[r] / s;
+      for (int r = 0; r < k; ++r) out_w[r] = ex[r] / sx;
     } else {
-      for (int r = 0; r < k; ++r) out_w[r] = sel_v[r];
+      float pr[16];
+      for (int r = 0; r < k; ++r) pr[r] = __expf(sel_v[r] - mx_all) / sum_all;
+      if (flags & MR_ROUTE_NORM_TOPK) {
+        float sx = 0.f;
+        for (int r = 0; r < k; ++r) sx = sx + pr[r];
+        for (int r = 0; r < k; ++r) out_w[r] = pr[r] / sx;
+      } else {
+        for (int r = 0; r < k; ++r) out_w[r] = pr[r];
+      }
     }
     for (int r = 0; r < k; ++r) out_idx[r] = sel_i[r];
   }

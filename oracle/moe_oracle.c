@@ -249,8 +249,12 @@ static void f32_matvec_mt(const float* w, const float* x, size_t out_features, s
 /* ---- routing: layer.rs:2346-2403 top_k_routing ---------------------------- */
 
 /* a ranks above b in the descending order: the larger number; a NaN ranks below every
- * number (the reference's partial_cmp -> Equal makes NaN order depend on its sort
- * algorithm, so this build fixes one rule for all paths). */
+ * number. The reference's comparator (partial_cmp -> Equal) calls a NaN equal to everything:
+ * where every value is NaN (standard mode: one NaN logit, a +inf maximum or a row of -inf makes
+ * every probability NaN) its stable sort keeps index order, which this rule reproduces (no
+ * value ranks above another, so the lowest remaining index is taken). A NaN among numbers
+ * (softmax-after-top-k mode) makes that comparator inconsistent and the reference's order
+ * depends on its sort algorithm; this build fixes NaN last for all paths. */
 static int ranks_above(float a, float b) {
   if (isnan(a)) return 0;
   if (isnan(b)) return 1;
