@@ -359,10 +359,12 @@ constexpr int kRouteVals = 8;  // experts per lane in routing: E <= 512
 // prob_exact_needed tells those rows apart; they are ranked again on the probabilities.
 // key: this lane's key columns (valid logits have keys >= 2, NaN 1, absent 0), T the k-th
 // largest key. The common answer costs a wave max and one compare pass.
+// NJ: the key columns that can be live (E <= 64 NJ).
+template <int NJ = kRouteVals>
 __device__ __forceinline__ bool prob_exact_needed(const uint32_t (&key)[kRouteVals], uint32_t T) {
   uint32_t mk = 0u;
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j) mk = max(mk, key[j]);
+  for (int j = 0; j < NJ; ++j) mk = max(mk, key[j]);
   const float lk = key_value(T), m = key_value(wave_max_u(mk)), d = m - lk;
   // lb >= lk - tau with tau = 2^-20 (1 + m - lb) <= 2^-20 (1 + m - lk) (1 + 2^-19): any key in
   // [key(lk - tau), T) is a near tie
@@ -372,7 +374,7 @@ __device__ __forceinline__ bool prob_exact_needed(const uint32_t (&key)[kRouteVa
   // near tie or a NaN (which makes every probability NaN; absent keys, 0, lie below lo).
   uint32_t hit = !(d <= 80.f) ? 1u : 0u;
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j)
+  for (int j = 0; j < NJ; ++j)
     hit |= ((key[j] >= lo ? 1u : 0u) & (key[j] < T ? 1u : 0u)) | (key[j] == 1u ? 1u : 0u);
   return __ballot(hit != 0u) != 0ull;
 }
@@ -531,16 +533,27 @@ struct RouteState {
   int my_e;
 };
 // The selection by key (topk_slots for one or two key columns, else topk_slots_wide) into
-// sel_i/sel_k; returns the k-th largest key.
+// sel_i/sel_k; returns the k-th largest key. CHECK: need = prob_exact_needed on the live
+// columns, computed while the slot stores drain.
+template <bool CHECK>
 __device__ __forceinline__ uint32_t select_keys(const uint32_t (&key)[kRouteVals], int nj, int k, int* sel_i,
-                                                uint32_t* sel_k, uint32_t* tmp) {
+                                                uint32_t* sel_k, uint32_t* tmp, bool& need) {
   const int lane = threadIdx.x & 63;
   int idx[kRouteVals];
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) idx[j] = lane + 64 * j;
-  const uint32_t T = nj <= 1   ? topk_slots<1>(key, idx, k, sel_i, sel_k)
-                     : nj <= 2 ? topk_slots<2>(key, idx, k, sel_i, sel_k)
-                               : topk_slots_wide(key, k, sel_i, sel_k, tmp);
+  uint32_t T;
+  need = false;
+  if (nj <= 1) {
+    T = topk_slots<1>(key, idx, k, sel_i, sel_k);
+    if (CHECK) need = prob_exact_needed<1>(key, T);
+  } else if (nj <= 2) {
+    T = topk_slots<2>(key, idx, k, sel_i, sel_k);
+    if (CHECK) need = prob_exact_needed<2>(key, T);
+  } else {
+    T = topk_slots_wide(key, k, sel_i, sel_k, tmp);
+    if (CHECK) need = prob_exact_needed(key, T);
+  }
   lds_drain();
   __builtin_amdgcn_wave_barrier();
   return T;
@@ -636,8 +649,9 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   for (int j = 0; j < kRouteVals; ++j)
     key[j] = (lane + 64 * j < rc.E) ? (v[j] == v[j] ? order_key(v[j] + 0.f) : 1u) : 0u;
   RTRACE(3);
-  const uint32_t T = select_keys(key, nj, rc.k, sel_i, sel_k, tmp);
-  if (QWEN && !(rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK) && prob_exact_needed(key, T)) {
+  bool need;
+  const uint32_t T = select_keys<QWEN>(key, nj, rc.k, sel_i, sel_k, tmp, need);
+  if (QWEN && need && !(rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK)) {
     const bool pnan = prob_keys(v, rc.E, key);
     prob_select(key, v, rc.E, rc.k, pnan, sel_i, sel_k);
   }
