@@ -417,10 +417,16 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       }
     }
     TRACE(1);
-    if (tid == 0) ok_flag = 1;
-    RouteState rs;  // wave 0: the selection, finished (weights, order) once its stream is issued
-    if (wave == 0 && !route_select<MR_ROUTE_SLEEP, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs)) {
-      if (lane == 0) ok_flag = 0, fail(a.err);
+    // The routing wave differs between the (up to four) workgroups that share a CU (workgroups
+    // b and b + 256 share one), so their polls and selections run on different SIMDs. It alone
+    // writes ok_flag: 0 exactly when the selection failed. The selection is finished (weights,
+    // order) once its stream is issued.
+    RouteState rs;
+    const int rw = (bid >> 8) & 3;
+    if (wave == rw) {
+      const bool routed = route_select<MR_ROUTE_SLEEP, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs);
+      if (lane == 0) ok_flag = routed ? 1 : 0;
+      if (!routed && lane == 0) fail(a.err);
     }
     XTRACE(wave);  // per wave: at the routing barrier
     __syncthreads();  // selection and x image ready
@@ -446,7 +452,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       (void)S;
       f32x4 dacc = stream_chain_v(W, (uint32_t)rb, nbH, lds_img + kStageOff + wave * 2 * kStageBytes, lds_img, lds_sc,
                                   lds_zero, lane, i, g, [&] {
-                                    if (wave == 0) route_finish(rc, rs, sel_w, sel_o);
+                                    if (wave == rw) route_finish(rc, rs, sel_w, sel_o);
                                   });
       XTRACE(4 + wave);  // per wave: chain done
       TRACE(3);
