@@ -23,11 +23,12 @@
 // Three groups of workgroups share one grid:
 //   [0, R)        router: one expert logit per wave; publishes it as a flagged
 //                 64-bit word (logit bits, launch number + 1).
-//   [R, R+ND)     down: 16 output rows; wave w takes slots w, w+4, ... (routed
-//                 slots, then the shared expert). The down weights of its first
-//                 slot are loaded into registers before the gate/up results exist,
-//                 so their HBM traffic overlaps the gate/up phase; a later slot's
-//                 are loaded once the previous slot is done (top_k > 4 only).
+//   [R, R+ND)     down: 16 output rows and a group of four slots; wave w takes slot
+//                 4 sg + w of slot group sg (routed slots, then the shared expert). Its
+//                 down weights are loaded into registers before the gate/up results
+//                 exist, so their HBM traffic overlaps the gate/up phase. With more than
+//                 four slots the row group's slot groups write partial rows and the last
+//                 of them to finish (a counter per row group) combines them.
 //   [R+ND, grid)  gate/up: 32 rows of one slot, both projections; 4 waves =
 //                 (gate, up) x 2 row tiles, each over the full K. The x split is
 //                 built in LDS while the router runs. Epilogue: bias, SwiGLU (SiLU

@@ -251,6 +251,61 @@ def test_topk_unnormalised_equals_full_softmax():
     assert np.allclose(w, np.take_along_axis(p, idx.astype(np.int64), 1), rtol=2e-6)
 
 
+def _prob_rank_f32(row, k):
+    """Standard-mode ranking written out as the reference does it (layer.rs:2371-2394): max by
+    f32::max (NaN ignored), p = exp(l - max) in f32, the sum in expert order, p / sum, then a
+    stable sort in which a NaN compares equal to everything (all-NaN rows keep expert order).
+    Only used on rows whose exp values are exact (0, 1, NaN) or far apart, so numpy's float32
+    exp and glibc's expf agree."""
+    finite = row[~np.isnan(row)]
+    m = np.float32(finite.max()) if finite.size else np.float32(-np.inf)
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = np.exp((row - m).astype(np.float32)).astype(np.float32)
+        tot = np.float32(0.0)
+        for v in e:
+            tot = np.float32(tot + v)
+        p = (e / tot).astype(np.float32)
+    if np.isnan(p).all():
+        order = np.arange(len(row))
+    else:
+        assert not np.isnan(p).any()
+        order = np.argsort(-p.astype(np.float64), kind="stable")
+    return order[:k], p
+
+
+@pytest.mark.parametrize("pattern", ["equal-probability", "underflow", "nan", "inf", "all-neg-inf"])
+def test_topk_standard_mode_ranks_probabilities(pattern):
+    """Distinct logits whose probabilities are equal tie (lower index first), not ranked by
+    logit; NaN probabilities (a NaN logit, a +inf maximum, a row of -inf) give experts 0..k-1
+    with NaN weights. Each pattern is checked to differ from ranking by logit."""
+    E, k = 40, 2 if pattern == "equal-probability" else 3
+    row = (np.random.default_rng(5).random(E) * 0.05).astype(np.float32)
+    if pattern == "equal-probability":   # expf(l - max) == 1.0f for all three
+        b = np.float32(0.125)
+        row[7], row[9], row[2] = b, b - np.spacing(b), b - 2 * np.spacing(b)
+    elif pattern == "underflow":         # expf(< -104) == 0: every other probability is 0
+        row = np.random.default_rng(6).uniform(-200, -150, E).astype(np.float32)
+        row[7] = 0.0
+    elif pattern == "nan":
+        row[5] = np.nan
+    elif pattern == "inf":
+        row[5] = np.inf
+    else:
+        row[:] = -np.inf
+    want, p = _prob_rank_f32(row, k)
+    by_logit = np.argsort(-row.astype(np.float64), kind="stable")[:k]
+    if pattern != "all-neg-inf":
+        assert set(want.tolist()) != set(by_logit.tolist())
+    for norm in (False, True):
+        idx, w = oracle.topk_routing(row[None, :], k, norm, False)
+        assert idx[0].tolist() == want.tolist(), (pattern, idx[0], want)
+        if pattern in ("nan", "inf", "all-neg-inf"):
+            assert idx[0].tolist() == list(range(k)) and np.isnan(w).all()
+        else:
+            ref = p[want] / (p[want].sum(dtype=np.float32) if norm else np.float32(1.0))
+            assert np.allclose(w[0], ref, rtol=1e-6, atol=0.0)
+
+
 # ---- activations -------------------------------------------------------------
 
 def test_silu_reference_kat():
