@@ -223,7 +223,8 @@ def trace_decode(a) -> None:
     tr = buf.download(np.uint64).reshape(1024, 32).astype(np.int64)
     grid = int(np.count_nonzero(tr[:, 0]))
     us = (tr[:grid] - tr[:grid, 0].min()) / 100.0
-    role = np.array(["router" if b < R else ("gateup" if R + ND <= b < R + ND + NG else "down") for b in range(grid)])
+    ridx = np.where(tr[:grid, 6] > 0, tr[:grid, 6] - 1, np.arange(grid))  # role index of each dispatch slot
+    role = np.array(["router" if b < R else ("gateup" if R + ND <= b < R + ND + NG else "down") for b in ridx])
 
     def q(v):
         return {"min": round(float(v.min()), 2), "median": round(float(np.median(v)), 2), "max": round(float(v.max()), 2)}

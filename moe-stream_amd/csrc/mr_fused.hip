@@ -86,6 +86,7 @@ struct FusedArgs {
   int NS;        // down row groups split into two 8-row workgroups (CU balance; at most four slots)
   int NDR, nsl;  // row groups and slot groups of the down role (ND = NDR * nsl)
   uint32_t spin_limit;
+  int perm_nc;  // CU count of the role permutation (role_index), 0: identity
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
   NormResid nr;               // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
@@ -314,7 +315,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int bid = blockIdx.x;
+  const int bid = role_index((int)blockIdx.x, a.perm_nc, a.R, a.ND, a.NG);  // role index
   const int nbH = a.H >> 5, nbI = a.I >> 5;
   TRACE(0);
   const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
@@ -418,12 +419,12 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       }
     }
     TRACE(1);
-    // The routing wave differs between the (up to four) workgroups that share a CU (workgroups
-    // b and b + 256 share one), so their polls and selections run on different SIMDs. It alone
-    // writes ok_flag: 0 exactly when the selection failed. The selection is finished (weights,
-    // order) once its stream is issued.
+    // The routing wave differs between the (up to four) workgroups that share a CU (dispatch
+    // slots b and b + 256 share one), so their polls and selections run on different SIMDs. It
+    // alone writes ok_flag: 0 exactly when the selection failed. The selection is finished
+    // (weights, order) once its stream is issued.
     RouteState rs;
-    const int rw = (bid >> 8) & 3;
+    const int rw = (int)(blockIdx.x >> 8) & 3;
     if (wave == rw) {
       const bool routed = route_select<MR_ROUTE_SLEEP, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs);
       if (lane == 0) ok_flag = routed ? 1 : 0;
@@ -624,6 +625,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   TRACE(5);
 #ifdef MR_FUSED_TRACE
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 6] = (unsigned long long)bid + 1;  // role index
   if (a.trace && (threadIdx.x & 63) == 0)  // HW_ID: wave, SIMD, CU, SE of each wave
     a.trace[blockIdx.x * 32 + 26 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
@@ -741,6 +743,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   const FusedGrid fg = fused_grid(L, n_cu);
   a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl;
+  a.perm_nc = role_perm_nc(fg.total(), fg.R, fg.NG, n_cu);
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;

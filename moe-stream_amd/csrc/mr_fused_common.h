@@ -46,6 +46,27 @@ inline uint64_t layer_sync_words(uint32_t n_logits) {
 // +1 at exit): all workgroups of a launch read the same value, with no atomic.
 __device__ __forceinline__ uint32_t* wg_seq_word(uint32_t* fs) { return fs + FS_WGSEQ + blockIdx.x; }
 
+// Role order of a fused launch: [routers R | down ND | gate/up NG | split down halves]. The
+// dispatcher hands workgroup b to CU b mod nc in round b / nc (one per CU per round, in index
+// order), so with the identity order the CUs that run two gate/up units can also get a down
+// group, and those gate/up units finish last. role_index maps the dispatch slot pb to a role
+// index so that they get nothing else: round 0 holds the routers and down groups on CUs
+// [0, nc - n2) and gate/up units on the other n2 = NG - nc CUs, round 1 a gate/up unit on every
+// CU, round 2 the remaining down groups (and split halves) on CUs [0, grid - 2 nc). Valid when
+// 2 nc <= grid <= 3 nc and nc <= NG <= 2 nc, with every router in round 0 (role_perm_nc); nc = 0
+// is the identity.
+__device__ __forceinline__ int role_index(int pb, int nc, int R, int ND, int NG) {
+  if (!nc) return pb;
+  const int r = pb / nc, c = pb - r * nc, n2 = NG - nc;
+  if (r == 1) return R + ND + n2 + c;
+  if (r == 0 && c >= nc - n2) return R + ND + (c - (nc - n2));
+  const int x = r == 0 ? c : (nc - n2) + c;  // the x-th router / down group / split half
+  return x < R + ND ? x : NG + x;
+}
+inline int role_perm_nc(int grid, int R, int NG, int n_cu) {
+  return (2 * n_cu <= grid && grid <= 3 * n_cu && n_cu <= NG && NG <= 2 * n_cu && R <= 2 * n_cu - NG) ? n_cu : 0;
+}
+
 __device__ __forceinline__ const uint8_t* expert_at(const ExpertLoc& l, int e) {
   return l.base + (l.tab ? l.tab[e] : (uint64_t)e * l.stride);
 }

@@ -306,6 +306,8 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches stay scalar
+  // role index = dispatch slot: the role permutation of the MXFP4 kernel (role_index) measured
+  // 4-5% slower on these grids, whose CUs with two gate/up units already hold nothing else
   const int bid = blockIdx.x;
   const int nsbH = a.H >> 8, nsbI = a.I >> 8, nGI = a.I >> 4;
   TRACE(0);
@@ -382,8 +384,9 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
     }
     // The routing wave goes straight to the logit poll, which the routing of every gate/up
     // workgroup waits on. It differs between the (up to four) workgroups that share a CU
-    // (workgroups b and b + 256 share one), so their polls and selections run on different SIMDs.
-    const int rw = (bid >> 8) & 3;
+    // (dispatch slots b and b + 256 share one), so their polls and selections run on different
+    // SIMDs.
+    const int rw = (int)(blockIdx.x >> 8) & 3;
     // x image: one 16-element group per thread of the other three waves
     for (int G = wave == rw ? -1 : (wave - (wave > rw ? 1 : 0)) * 64 + lane; G < (a.H >> 4); G += 192) {
       if (G < 0) break;
@@ -628,6 +631,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
   TRACE(5);
 #ifdef MR_FUSED_TRACE
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 7] = __smid();
+  if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * 32 + 6] = (unsigned long long)bid + 1;  // role index
   if (a.trace && (threadIdx.x & 63) == 0)  // HW_ID: wave, SIMD, CU, SE of each wave
     a.trace[blockIdx.x * 32 + 26 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
