@@ -86,6 +86,7 @@ struct FusedArgs {
   int NS;        // down row groups split into two 8-row workgroups (CU balance; at most four slots)
   int NDR, nsl;  // row groups and slot groups of the down role (ND = NDR * nsl)
   uint32_t spin_limit;
+  int dn_delay;  // s_sleep(8) rounds before the down role's weight prefetch (dn_delay_rounds)
   int perm_nc;  // CU count of the role permutation (role_index), 0: identity
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
@@ -523,6 +524,9 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const int slot = sg * 4 + wave;  // this wave's slot (routed, then the shared expert)
       const int sl = min(slot, ktot - 1);
       const uint8_t* D = (sl >= a.k ? a.sh_down : expert_at(a.down, sel_i[sl])) + (uint64_t)row * rb;
+      // the prefetch waits a while: issued at once, its bytes share HBM with the gate/up
+      // streams from the start and delay the last gate/up units, which set the hand-off
+      for (int it = 0; it < a.dn_delay; ++it) __builtin_amdgcn_s_sleep(8);
       if (slot < ktot) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
@@ -717,6 +721,18 @@ bool fused_resident(const mr_layer& L, int n_cu) {
   return (int64_t)std::min(b0, b1) * n_cu >= fused_grid(L, n_cu).total();
 }
 
+// Delay of the down role's weight prefetch, in s_sleep(8) rounds (512 clocks, about 0.21 us at
+// 2.4 GHz): 30% of the gate/up stream time, estimated from the gate/up bytes at the measured
+// stream rate (4.2 TB/s). On C2 (35 MB of gate/up rows, 2.5 us) +1.8% over no delay; the gain
+// grows up to about 3 us and turns into a loss beyond 4 us (the down weights then arrive after
+// the hand-off), so the setting keeps a margin. Plain layers only (top-k <= 4, no shared expert),
+// where it was measured.
+static int dn_delay_rounds(const mr_layer& L) {
+  if (fused_gen(L)) return 0;
+  const double gu_bytes = 2.0 * (double)L.d.top_k * (double)L.I * (double)(L.H / 32) * 17.0;
+  return (int)(0.30 * gu_bytes / 4.2e6 / 0.213 + 0.5);
+}
+
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
                         uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
                         const NormResid& nr) {
@@ -744,6 +760,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   const FusedGrid fg = fused_grid(L, n_cu);
   a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl;
   a.perm_nc = role_perm_nc(fg.total(), fg.R, fg.NG, n_cu);
+  a.dn_delay = dn_delay_rounds(L);
   a.spin_limit = spin_limit;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
