@@ -67,7 +67,7 @@ extern "C" {
 #define MR_DECODE_AUTO 0   /* fastest available */
 #define MR_DECODE_VALU 1   /* vector-ALU dequant-matvec kernels, one launch per step */
 #define MR_DECODE_FUSED 2  /* single fused launch per layer: router, top-k, experts, combine
-                              (MXFP4 on scaled MX-fp4 MFMA; Q4_K on int8 dot products) */
+                              (MXFP4 on the scaled MX-fp4 MFMA; Q4_K on the int8 MFMA) */
 /* 1: record a HIP event pair around every kernel launch (read with mr_profile_read). */
 #define MR_OPT_PROFILE 2
 /* Iteration limit of the fused decode kernel's cross-workgroup waits (default

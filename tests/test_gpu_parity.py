@@ -126,6 +126,10 @@ WIDE_MX = {
                             True, True),
     "mxfp4-k16-shared": W.LayerSpec(220, 0, W.GGML_MXFP4, 512, 256, 32, 16, W.ROUTE_NORM_TOPK, W.ACT_SILU, False,
                                     False, sh_inter=256, sh_type=W.GGML_MXFP4),
+    # 713 workgroups (17 routers, 180 row groups x 2 slot groups, 336 gate/up units): the grid
+    # takes the role permutation of the dispatch slots, with slot groups and a shared expert
+    "mxfp4-k6-shared-H2880": W.LayerSpec(221, 0, W.GGML_MXFP4, 2880, 1536, 64, 6, W.ROUTE_NORM_TOPK,
+                                         W.ACT_SWIGLU_OAI, True, True, sh_inter=1536, sh_type=W.GGML_MXFP4),
 }
 SPECS = {
     **WIDE_Q4,
