@@ -643,8 +643,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         # what the kernels compute: MXFP4 weights on the scaled MFMA against the activation
-        # split into 4 e4m3 terms per 32-element block; Q4_K weights on int8 dot products
-        # against the activation split into 2 int8 terms per 16-element group; f32 accumulation
+        # split into 4 e4m3 terms per 32-element block; Q4_K weights on the int8 MFMA against
+        # the activation split into 2 int8 terms per 16-element group (int32 sums, f32 scaling)
         "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if s0.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1))",
         "config": {"workload": W.CONFIG_NAMES[a.config], "config_id": a.config,
