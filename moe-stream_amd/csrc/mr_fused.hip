@@ -543,7 +543,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       if (slot < ktot)  // waits for the weights: they land long before gate/up ends
         prep_rows(rd, (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u, nbI, g);
       TRACE(2);
-      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 64>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit) && lane == 0)
+      // polled every 4 sleep units once at most an eighth of the units are missing (+0.3%)
+      if (wave == 0 &&
+          !wait_count<MR_GU_WAIT_SLEEP, 64, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit, (uint32_t)a.NG / 8) &&
+          lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
       TRACE(3);
