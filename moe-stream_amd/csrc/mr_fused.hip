@@ -725,15 +725,16 @@ bool fused_resident(const mr_layer& L, int n_cu) {
 }
 
 // Delay of the down role's weight prefetch, in s_sleep(8) rounds (512 clocks, about 0.21 us at
-// 2.4 GHz): 30% of the gate/up stream time, estimated from the gate/up bytes at the measured
-// stream rate (4.2 TB/s). On C2 (35 MB of gate/up rows, 2.5 us) +1.8% over no delay; the gain
-// grows up to about 3 us and turns into a loss beyond 4 us (the down weights then arrive after
-// the hand-off), so the setting keeps a margin. Plain layers only (top-k <= 4, no shared expert),
-// where it was measured.
+// 2.4 GHz): a quarter of the gate/up stream time, estimated from the gate/up bytes at the
+// measured stream rate (4.2 TB/s). Swept on C2 (35 MB of gate/up rows) as a fraction of that
+// estimate: 0.2 +1.3%, 0.3 and 0.4 +1.8%, 0.5 -4.7% (the down weights then arrive after the
+// hand-off). 0.25 stays well below that edge should the shader clock run lower (a lower clock
+// lengthens the same number of sleep rounds). Plain layers only (top-k <= 4, no shared
+// expert), where it was measured.
 static int dn_delay_rounds(const mr_layer& L) {
   if (fused_gen(L)) return 0;
   const double gu_bytes = 2.0 * (double)L.d.top_k * (double)L.I * (double)(L.H / 32) * 17.0;
-  return (int)(0.30 * gu_bytes / 4.2e6 / 0.213 + 0.5);
+  return (int)(0.25 * gu_bytes / 4.2e6 / 0.213 + 0.5);
 }
 
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
