@@ -96,6 +96,43 @@ def test_probability_ties_take_the_lower_index(gpu_ctx, name, pattern):
         assert want == by_logit(b, k)
     if pattern in ("nan-logit", "inf-logit"):
         assert want == set(range(k)) and np.isnan(rw).all()
+    _check_every_path(gpu_ctx, spec, host, k, want, ridx, rw)
+
+
+# The softmax-after-top-k (GPT-OSS) mode ranks raw logits with the same comparator. Where that
+# order is fixed whatever the sort algorithm: a row of NaN (every comparison "equal": experts
+# 0..k-1) and a +inf logit (ranked first; its weight exp(inf - inf) makes every weight NaN).
+OAI_PATTERNS = {"all-nan": 3, "inf-logit": 3}
+
+
+@pytest.mark.parametrize("pattern", list(OAI_PATTERNS))
+def test_softmax_after_topk_nan_and_inf_rows(gpu_ctx, pattern):
+    k = OAI_PATTERNS[pattern]
+    spec = W.LayerSpec(233, 0, W.GGML_MXFP4, 256, 128, 32, k, W.ROUTE_SOFTMAX_AFTER_TOPK, W.ACT_SWIGLU_OAI,
+                       True, True)
+    host = dict(spec=spec)
+    host.update(W.quant_tensors(spec))
+    host.update(W.float_tensors(spec))
+    host["router_w"] = np.zeros_like(host["router_w"])
+    b = (np.random.default_rng(13).random(spec.n_experts) * 0.05).astype(np.float32)
+    if pattern == "all-nan":
+        b[:] = np.nan
+    else:
+        b[5] = np.inf
+    host["router_b"] = b
+    ridx, rw = oracle.topk_routing(b[None, :], k, False, True)
+    want = set(ridx[0].tolist())
+    if pattern == "all-nan":
+        assert want == set(range(k))
+    else:
+        assert 5 in want and want == by_logit(b, k)
+    assert np.isnan(rw).all()
+    _check_every_path(gpu_ctx, spec, host, k, want, ridx, rw)
+
+
+def _check_every_path(gpu_ctx, spec, host, k, want, ridx, rw):
+    """The selection `want` and the oracle's weights and outputs on every device path: the
+    multi-kernel routing (one token and 32), fused and multi-kernel decode, the batched path."""
     dl = W.DeviceLayer(gpu_ctx, spec, host=host)
     L = oracle.layer_from_host(host)
     try:
