@@ -114,13 +114,18 @@ def copy_calibration(n_bytes: int = 1 << 30, reps: int = 4) -> None:
 
 
 def probes() -> None:
-    """Ceilings of the decode path on this GPU, with the library's probe kernels:
-    - kernel boundary: a HIP graph of 24 empty kernels (as a token's graph holds 24 layer
-      launches) with the C2 fused kernel's grid and with one workgroup, time per kernel;
-    - plain stream: mr_probe_read over the byte count of one C2 layer (53.4 MB), of its gate/up
-      weights (35.2 MB) and of one C3 layer (22.3 MB), with the C2 fused grid's workgroup count
-      and with 2048, reading in turn from 8 buffers (427 MB, beyond the 256 MB Infinity Cache)
-      so that every read comes from HBM."""
+    """Ceilings of the decode path on this GPU, with the library's probe kernels, every
+    launch inside a HIP graph as in the timed decode:
+    - kernel boundary: a graph of 24 empty kernels (a token's graph holds 24 layer launches)
+      with the C2 fused kernel's grid and with one workgroup, time per kernel;
+    - plain stream: mr_probe_read (each workgroup a contiguous range, 4, 8 or 16 16-byte loads
+      in flight per thread) over byte counts from 2.2 MB to 214 MB, among them one C2 layer's
+      53.4 MB, its gate/up weights' 35.2 MB and one C3 layer's 22.3 MB, with 256 to 2048
+      workgroups. One graph holds n launches reading consecutive regions of a 1.5 GiB pool
+      (n x bytes >= 768 MB, beyond the 256 MB Infinity Cache), so every byte comes from HBM.
+      Per (grid, depth): the least-squares fit t = t0 + bytes / B over the sizes, which splits a
+      launch into its fixed cost t0 (launch in the graph, ramp, first-touch latency, drain) and
+      the sustained rate B; and a 1 GiB read per launch as a check of B."""
     import moe_rocm as M
     from moe_rocm import workloads as W
 
@@ -128,8 +133,8 @@ def probes() -> None:
     c2 = W.gpt_oss(2, 0)
     c2_bytes, c3_bytes = c2.weight_bytes_per_token(), W.qwen3_30b(3, 0).weight_bytes_per_token()
     gu_bytes = c2.top_k * 2 * M.synth.matrix_bytes(c2.ggml_type, c2.inter, c2.hidden)
-    fused_grid = 576  # C2: 8 router + 180 down + 360 gate/up + 28 split down workgroups
-    out = {"probe": "decode ceilings", "gpu_workgroups_c2_fused": fused_grid}
+    fused_grid = 576  # C2 fused kernel
+    out = {"probe": "decode ceilings", "method": "HIP graphs; event time over the graph / launches"}
     floor = {}
     for n_wg in (fused_grid, 1):
         ctx.graph_begin()
@@ -147,30 +152,97 @@ def probes() -> None:
         g.close()
         floor[str(n_wg)] = round(ms * 1e3 / (reps * 24), 3)
     out["empty_kernel_in_graph_us"] = floor
-    n_buf = 8
-    size = (c2_bytes + 4095) // 4096 * 4096
-    bufs = [ctx.alloc(size) for _ in range(n_buf)]
-    for b in bufs:
-        ctx.synth_blocks(M.GGML_MXFP4, b, size // 17, 7)
+    pool_bytes = 1536 << 20
+    pool = ctx.alloc(pool_bytes)
+    ctx.synth_blocks(M.GGML_MXFP4, pool, pool_bytes // 17, 7)
     sink = ctx.alloc(4 * 4096)
-    reads = []
-    for name, nbytes in (("c2_layer", c2_bytes), ("c2_gate_up", gu_bytes), ("c3_layer", c3_bytes)):
-        nbytes = nbytes // 16 * 16
-        for n_wg in (fused_grid, 2048):
-            for i in range(n_buf):
-                ctx.probe_read(bufs[i], nbytes, n_wg, sink)
+    named = {"c2_layer": c2_bytes // 16 * 16, "c2_gate_up": gu_bytes // 16 * 16, "c3_layer": c3_bytes // 16 * 16}
+    sizes = sorted(set([s // 16 * 16 for s in (2_200_000, 4_406_400, 8_812_800, 17_625_600, 106_813_696,
+                                               213_627_392)] + list(named.values())))
+    pts = []
+    fits = {}
+    for n_wg in (256, 512, 768, 1024, 2048):
+        for depth in (4, 8, 16):
+            xs, ys = [], []
+            for nbytes in sizes:
+                n = max(24, -(-(768 << 20) // nbytes))
+                stride = (nbytes + 4095) // 4096 * 4096
+                n = min(n, (pool_bytes - stride) // stride + 1)
+                ctx.graph_begin()
+                for i in range(n):
+                    ctx.probe_read(pool.ptr + i * stride, nbytes, n_wg, sink, depth=depth)
+                g = ctx.graph_end()
+                g.launch()
+                ctx.sync()
+                reps = 3
+                ctx.timer_start()
+                for _ in range(reps):
+                    g.launch()
+                ms = ctx.timer_stop()
+                g.close()
+                us = ms * 1e3 / (reps * n)
+                name = next((k for k, v in named.items() if v == nbytes), None)
+                pts.append({"workgroups": n_wg, "depth": depth, "nbytes": nbytes, "bytes": name,
+                            "launches_per_graph": n, "us": round(us, 3),
+                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+                xs.append(nbytes)
+                ys.append(us)
+            A = np.vstack([np.ones(len(xs)), np.asarray(xs, np.float64)]).T
+            (t0, inv_b), *_ = np.linalg.lstsq(A, np.asarray(ys, np.float64), rcond=None)
+            resid = float(np.max(np.abs(A @ np.array([t0, inv_b]) - np.asarray(ys))))
+            fits[f"{n_wg}x{depth}"] = {"workgroups": n_wg, "depth": depth, "t0_us": round(float(t0), 3),
+                                       "B_GB_per_s": round(1e-3 / inv_b, 1), "max_resid_us": round(resid, 3),
+                                       "c2_layer_floor_us": round(float(t0 + inv_b * named["c2_layer"]), 3)}
+            log(f"fit {n_wg} wg x depth {depth}: t0 {t0:.2f} us, B {1e-3 / inv_b:.0f} GB/s")
+    out["plain_read"] = pts
+    out["fit_t0_plus_bytes_over_B"] = fits
+    # the gate/up access pattern of the fused MXFP4 kernel over the same bytes as C2's gate/up
+    # weights (4 experts x 2 projections x 2880 rows of 1530 bytes = 1440 tiles of 16 rows)
+    rb = 1530
+    n_tiles = gu_bytes // (16 * rb)
+    tile_bytes = n_tiles * 16 * rb
+    stride = (tile_bytes + 4095) // 4096 * 4096
+    tiles = []
+    for n_wg in (256, 512, 768):
+        for depth in (2, 4, 8, 0x106, 0x10C, 0x117):
+            n = min(max(24, -(-(768 << 20) // tile_bytes)), (pool_bytes - stride) // stride + 1)
+            ctx.graph_begin()
+            for i in range(n):
+                ctx.probe_tiles(pool.ptr + i * stride, rb, n_tiles, n_wg, sink, depth=depth)
+            g = ctx.graph_end()
+            g.launch()
             ctx.sync()
-            reps = 64
             ctx.timer_start()
-            for i in range(reps):
-                ctx.probe_read(bufs[i % n_buf], nbytes, n_wg, sink)
+            for _ in range(3):
+                g.launch()
             ms = ctx.timer_stop()
-            us = ms * 1e3 / reps
-            reads.append({"bytes": name, "nbytes": nbytes, "workgroups": n_wg, "us": round(us, 3),
-                          "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
-    out["plain_read"] = reads
-    for b in bufs + [sink]:
-        b.free()
+            g.close()
+            us = ms * 1e3 / (3 * n)
+            tiles.append({"workgroups": n_wg, "depth": depth if depth < 0x100 else 1,
+                          "chunk_steps": 3 if depth < 0x100 else depth - 0x100, "nbytes": tile_bytes, "us": round(us, 3),
+                          "GB_per_s": round(tile_bytes / (us * 1e-6) / 1e9, 1)})
+            log(f"tiles {n_wg} wg x depth {depth}: {us:.2f} us, {tile_bytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    out["gateup_tile_pattern_read"] = tiles
+    big = []
+    for n_wg in (1024, 2048):
+        for depth in (8, 16):
+            nbytes = 1 << 30
+            ctx.graph_begin()
+            ctx.probe_read(pool.ptr, nbytes, n_wg, sink, depth=depth)
+            ctx.probe_read(pool.ptr + (pool_bytes - nbytes) // 4096 * 4096, nbytes, n_wg, sink, depth=depth)
+            g = ctx.graph_end()
+            g.launch()
+            ctx.sync()
+            ctx.timer_start()
+            for _ in range(3):
+                g.launch()
+            ms = ctx.timer_stop()
+            g.close()
+            us = ms * 1e3 / 6
+            big.append({"workgroups": n_wg, "depth": depth, "nbytes": nbytes, "us": round(us, 1),
+                        "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    out["read_1GiB"] = big
+    pool.free(), sink.free()
     ctx.close()
     print(json.dumps(out), flush=True)
 

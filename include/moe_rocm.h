@@ -70,10 +70,13 @@ extern "C" {
                               (MXFP4 on the scaled MX-fp4 MFMA; Q4_K on the int8 MFMA) */
 /* 1: record a HIP event pair around every kernel launch (read with mr_profile_read). */
 #define MR_OPT_PROFILE 2
-/* Iteration limit of the fused decode kernel's cross-workgroup waits (default
- * 2^22, about 0.1 s). A wait that runs out ends the launch early and makes the
- * next mr_sync return MR_E_LAUNCH; a value of 0 restores the default. */
-#define MR_OPT_SPIN_LIMIT 3
+/* Time limit in microseconds of each cross-workgroup wait inside the fused decode
+ * kernels (default 50000, i.e. 50 ms), measured on the device's constant-rate clock.
+ * A wait that runs out ends the launch early and makes the next mr_sync return
+ * MR_E_LAUNCH. A wait consults the clock from its 64th poll on (limits below 100 us:
+ * from its first), so it gives up at most about 1 ms after the limit; a value of 0
+ * restores the default. */
+#define MR_OPT_WAIT_LIMIT_US 3
 
 typedef struct mr_ctx mr_ctx;
 typedef struct mr_pack mr_pack;
@@ -301,21 +304,8 @@ int mr_timer_stop(mr_ctx* ctx, float* out_ms);
 int mr_profile_read(mr_ctx* ctx, const char* kernel, uint64_t* out_count, double* out_total_ms);
 int mr_profile_reset(mr_ctx* ctx);
 
-/* ---- synthetic inputs (bench/test support, not a reference interface) ------ */
-/* Fill device bytes with the counter-based SplitMix64 generator of
- * moe_rocm/synth.py: MXFP4 blocks (e8m0 uniform in [119,127], nibbles uniform)
- * or Q4_K super-blocks (fp16 d ~|N(0,0.01)|, dmin ~|N(0,0.005)| by the
- * Irwin-Hall(12) construction, scale and quant bytes uniform). */
-int mr_synth_blocks(mr_ctx* ctx, int ggml_type, void* dst, uint64_t n_blocks, uint64_t seed);
-
-/* ---- measurement probes (bench support, not a reference interface) ------------ */
-/* A plain streaming read of nbytes (a multiple of 16) from src by n_workgroups workgroups of
- * 256 threads (16-byte loads, four in flight per thread; one word per workgroup is written to
- * sink [n_workgroups] u32), and an empty kernel of n_workgroups workgroups: the ceilings the
- * decode kernels are measured against (the bytes a plain stream moves per microsecond, the
- * cost of a kernel boundary). Profile names "probe_read" and "probe_empty". */
-int mr_probe_read(mr_ctx* ctx, const void* src, uint64_t nbytes, uint32_t n_workgroups, uint32_t* sink);
-int mr_probe_empty(mr_ctx* ctx, uint32_t n_workgroups);
+/* Bench and test support (synthetic weights, measurement probes) is declared in
+ * moe_rocm_bench.h; it is not part of this interface. */
 
 #ifdef __cplusplus
 }

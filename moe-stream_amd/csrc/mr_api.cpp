@@ -292,6 +292,8 @@ int mr_ctx_create(int device, mr_ctx** out) {
   if (e == hipSuccess) e = hipEventCreate(&c->ev0);
   if (e == hipSuccess) e = hipEventCreate(&c->ev1);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
+  if (e == hipSuccess && hipDeviceGetAttribute(&c->wall_khz, hipDeviceAttributeWallClockRate, device) != hipSuccess)
+    c->wall_khz = 100000;  // the documented 100 MHz when the runtime does not report it
   if (e != hipSuccess) {
     int rc = hip_fail(nullptr, e, "context setup");
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -347,9 +349,9 @@ int mr_ctx_set_option(mr_ctx* c, int option, int value) {
     c->decode_kernel = value;
     return MR_OK;
   }
-  if (option == MR_OPT_SPIN_LIMIT) {
-    if (value < 0) return set_err(c, MR_E_INVAL, "spin limit %d is negative", value);
-    c->spin_limit = value == 0 ? (1u << 22) : (uint32_t)value;
+  if (option == MR_OPT_WAIT_LIMIT_US) {
+    if (value < 0) return set_err(c, MR_E_INVAL, "wait limit %d us is negative", value);
+    c->wait_limit_us = value == 0 ? 50000u : (uint32_t)value;
     return MR_OK;
   }
   if (option == MR_OPT_PROFILE) {
@@ -693,7 +695,7 @@ static int forward_one(mr_ctx* c, const mr_layer* L, const float* x, float* y, c
     uint8_t* img = static_cast<uint8_t*>(s.mfma_b);
     if (mr::fused_supported(*L, c->n_cu)) {
       c->fused_used = true;
-      e = mr::launch_fused(c->launch(), *L, x, y, err, img, c->spin_limit, c->n_cu, nr);
+      e = mr::launch_fused(c->launch(), *L, x, y, err, img, mr::wait_bound(*c), c->n_cu, nr);
       return e == hipSuccess ? MR_OK : hip_fail(c, e, "fused moe forward launch");
     }
     if (mr::fused_q4k_supported(*L, c->n_cu)) {
@@ -834,15 +836,29 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "batched moe launch (static scratch)");
 }
 
-int mr_probe_read(mr_ctx* c, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t* sink) {
+int mr_probe_read(mr_ctx* c, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t depth, uint32_t* sink) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   if (!src || !sink || n_wg == 0 || nbytes % 16 != 0) return set_err(c, MR_E_INVAL, "probe_read: bad arguments");
+  if (depth != 4 && depth != 8 && depth != 16) return set_err(c, MR_E_INVAL, "probe_read: depth must be 4, 8 or 16");
   if (misaligned(src, 16)) return set_err(c, MR_E_INVAL, "probe_read: src must be 16-byte aligned");
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   int rc = bind(c);
   if (rc) return rc;
-  const hipError_t e = mr::launch_probe_read(c->launch(), src, nbytes, n_wg, sink);
+  const hipError_t e = mr::launch_probe_read(c->launch(), src, nbytes, n_wg, depth, sink);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_read launch");
+}
+
+int mr_probe_tiles(mr_ctx* c, const void* src, uint32_t row_bytes, uint32_t n_tiles, uint32_t n_wg, uint32_t depth,
+                   uint32_t* sink) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!src || !sink || n_wg == 0 || row_bytes < 16 || n_tiles == 0) return set_err(c, MR_E_INVAL, "probe_tiles: bad arguments");
+  if (depth != 2 && depth != 4 && depth != 8 && depth != 0x106 && depth != 0x10C && depth != 0x117)
+    return set_err(c, MR_E_INVAL, "probe_tiles: depth must be 2, 4, 8 or 0x100 + 6, 12, 23");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  const hipError_t e = mr::launch_probe_tiles(c->launch(), src, row_bytes, n_tiles, n_wg, depth, sink);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_tiles launch");
 }
 
 int mr_probe_empty(mr_ctx* c, uint32_t n_wg) {

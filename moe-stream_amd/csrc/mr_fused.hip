@@ -43,7 +43,7 @@
 // down B image is announced by a monotonic counter (64 copies) bumped after the
 // image stores have completed. Each workgroup keeps its own launch number (read at
 // entry, stored +1 at exit), so nothing is reset between launches. Every wait is
-// bounded (the context's spin limit); a wait that runs out sets an error word read
+// bounded in time (the context's wait limit); a wait that runs out sets an error word read
 // at mr_sync and the launch still exits.
 #include "mr_device.h"
 #include "mr_internal.h"
@@ -85,7 +85,7 @@ struct FusedArgs {
   int R, NG, ND;
   int NS;        // down row groups split into two 8-row workgroups (CU balance; at most four slots)
   int NDR, nsl;  // row groups and slot groups of the down role (ND = NDR * nsl)
-  uint32_t spin_limit;
+  WaitBound wb;  // time limit of the cross-workgroup waits
   int dn_delay;  // s_sleep(8) rounds before the down role's weight prefetch (dn_delay_rounds)
   int perm_nc;  // CU count of the role permutation (role_index), 0: identity
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   TRACE(0);
   const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
   const int has_sh = GEN ? a.has_sh : 0, ktot = GEN ? a.ktot : a.k;
-  const RouteCfg rc{a.fs, (uint32_t)(a.E + has_sh), a.E, a.k, a.flags, a.spin_limit, a.trace};
+  const RouteCfg rc{a.fs, (uint32_t)(a.E + has_sh), a.E, a.k, a.flags, a.wb, a.trace};
   if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
 
   if (bid < a.R) {
@@ -516,6 +516,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     if (wave == 0) __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     TRACE(1);
+    float yres = 0.f, ybias = 0.f;  // this thread's output-row residual and bias terms (tid < 16)
     if (ok_flag) {
       const int S = (nbI + 3) >> 2;
       const int row = q * 16 + (half == 0 ? i : (half == 2 ? 8 : 0) + (i & 7));
@@ -536,8 +537,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         for (int p = 0; p < 4; ++p) so[p] = sel_o[min(p, a.k - 1)] * 16;
       }
       // this thread's output-row bias terms and residual, also independent of gate/up
-      const float yres = (tid < 16 && NORM && q * 16 + tid < a.H) ? a.nr.resid[q * 16 + tid] : 0.f;
-      float ybias = 0.f;
+      if (tid < 16 && NORM && q * 16 + tid < a.H) yres = a.nr.resid[q * 16 + tid];
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       if (slot < ktot)  // waits for the weights: they land long before gate/up ends
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       TRACE(2);
       // polled every 4 sleep units once at most an eighth of the units are missing (+0.3%)
       if (wave == 0 &&
-          !wait_count<MR_GU_WAIT_SLEEP, 64, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit, (uint32_t)a.NG / 8) &&
+          !wait_count<MR_GU_WAIT_SLEEP, 64, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.wb, (uint32_t)a.NG / 8) &&
           lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
@@ -601,29 +601,34 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
             if (rr < a.H) a.y[rr] = yv;
             XTRACE(8);
           }
-        } else {
-          // this slot group's rows -> the partials buffer; the row group's last slot group to
-          // finish (a counter per row group, nothing waits) combines every slot
-          if (tid < 64 && sg * 4 + (tid >> 4) < ktot) {
-            st_sc1(reinterpret_cast<uint32_t*>(a.dpart) + (size_t)(sg * 4 + (tid >> 4)) * a.H + q * 16 + (tid & 15),
-                   __float_as_uint(lds_part[tid]));
-            vm_drain();  // partials complete before the count that announces them
-          }
-          __syncthreads();
-          if (tid == 0)
-            ok_flag = add_sc1(a.fs + FS_DN + q, 1u) + 1u == (seq + 1u) * (uint32_t)a.nsl ? 2 : 1;
-          __syncthreads();
-          if (ok_flag == 2 && tid < 16) {
-            const int rr = q * 16 + tid;
-            const uint32_t* part = reinterpret_cast<const uint32_t*>(a.dpart);
-            float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
-            for (int p = 0; p < a.k; ++p) yv = yv + __uint_as_float(ld_sc1(part + (size_t)sel_o[p] * a.H + rr));
-            yv = yv + ybias;
-            if (has_sh) yv = yv + __uint_as_float(ld_sc1(part + (size_t)a.k * a.H + rr));  // shared expert last
-            if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
-            a.y[rr] = yv;
-          }
+        } else if (tid < 64 && sg * 4 + (tid >> 4) < ktot) {
+          // this slot group's rows -> the partials buffer (combined below)
+          st_sc1(reinterpret_cast<uint32_t*>(a.dpart) + (size_t)(sg * 4 + (tid >> 4)) * a.H + q * 16 + (tid & 15),
+                 __float_as_uint(lds_part[tid]));
+          vm_drain();  // partials complete before the count that announces them
         }
+      }
+    }
+    if (GEN && a.nsl > 1) {
+      // The row group's last slot group to finish (a counter per row group, nothing waits)
+      // combines every slot. Every slot group counts, also one whose routing or gate/up wait
+      // ran out (that launch is reported failed), so the counter stays in step with the launch
+      // number for the launches after it.
+      __syncthreads();
+      if (tid == 0) {
+        const bool last = add_sc1(a.fs + FS_DN + q, 1u) + 1u == (seq + 1u) * (uint32_t)a.nsl;
+        ok_flag = ok_flag && last ? 2 : 0;
+      }
+      __syncthreads();
+      if (ok_flag == 2 && tid < 16) {
+        const int rr = q * 16 + tid;
+        const uint32_t* part = reinterpret_cast<const uint32_t*>(a.dpart);
+        float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
+        for (int p = 0; p < a.k; ++p) yv = yv + __uint_as_float(ld_sc1(part + (size_t)sel_o[p] * a.H + rr));
+        yv = yv + ybias;
+        if (has_sh) yv = yv + __uint_as_float(ld_sc1(part + (size_t)a.k * a.H + rr));  // shared expert last
+        if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
+        a.y[rr] = yv;
       }
     }
   }
@@ -721,7 +726,21 @@ bool fused_resident(const mr_layer& L, int n_cu) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, fused_kernel<false>(L), 256, lds) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, fused_kernel<true>(L), 256, lds) != hipSuccess)
     return false;
-  return (int64_t)std::min(b0, b1) * n_cu >= fused_grid(L, n_cu).total();
+  const int grid = fused_grid(L, n_cu).total();
+  if ((int64_t)std::min(b0, b1) * n_cu < grid) return false;
+  // The occupancy the runtime reports has been seen to count LDS more finely than the CU
+  // allocates it (three workgroups of 53.8 KB, reported to fit the 160 KB of a CU, did not all
+  // start): a workgroup's LDS, static and dynamic, rounded up to 2 KB, times the workgroups one
+  // CU must hold, must fit as well.
+  int dev = 0, cu_lds = 0;
+  hipFuncAttributes fa{}, fb{};
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cu_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      hipFuncGetAttributes(&fa, fused_kernel<false>(L)) != hipSuccess ||
+      hipFuncGetAttributes(&fb, fused_kernel<true>(L)) != hipSuccess)
+    return false;
+  const size_t wg_lds = (std::max(fa.sharedSizeBytes, fb.sharedSizeBytes) + lds + 2047) & ~(size_t)2047;
+  return (int64_t)wg_lds * ((grid + n_cu - 1) / n_cu) <= (int64_t)cu_lds;
 }
 
 // Delay of the down role's weight prefetch, in s_sleep(8) rounds (512 clocks, about 0.21 us at
@@ -738,7 +757,7 @@ static int dn_delay_rounds(const mr_layer& L) {
 }
 
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
+                        uint32_t* err, uint8_t* img_base, WaitBound wb, int n_cu,
                         const NormResid& nr) {
   FusedArgs a{};
 #ifdef MR_FUSED_TRACE
@@ -765,7 +784,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl;
   a.perm_nc = role_perm_nc(fg.total(), fg.R, fg.NG, n_cu);
   a.dn_delay = dn_delay_rounds(L);
-  a.spin_limit = spin_limit;
+  a.wb = wb;
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
   a.lds_img_bytes = (uint32_t)fused_lds_img_bytes(L);

@@ -10,8 +10,8 @@
 //    launches. Producers increment one of kCopies copies (spread over separate
 //    cache lines) without waiting for a return value; waiters sum the copies.
 //    Each workgroup keeps its own launch number n (no exit atomic);
-//  * bounded waits: a wait that runs out of iterations sets the context error
-//    word (read and cleared by mr_sync) and the launch still exits normally.
+//  * bounded waits: a wait that runs past its time limit (device clock) sets the
+//    context error word (read and cleared by mr_sync) and the launch still exits normally.
 #pragma once
 
 #include "../../include/moe_rocm.h"
@@ -228,6 +228,27 @@ __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" :
 // All LDS operations this wave has issued have completed.
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Time limit of a cross-workgroup wait, on the device's constant-rate clock (wall_clock64,
+// s_memrealtime). `free` polls come without a clock read (every wait of a normal launch ends
+// well within them); from then on every poll reads the clock and compares the reading of the
+// poll before with the clock at poll `free`, so no poll waits for its own clock read. A wait
+// therefore gives up at most `free` polls plus `ticks` after it began.
+// (WaitBound, the launch argument: mr_internal.h.)
+struct WaitTimer {
+  uint64_t t0 = 0, t1 = 0;
+  // at poll `it` of a wait: whether the limit has passed
+  __device__ __forceinline__ bool out(uint32_t it, const WaitBound& b) {
+    if (it < b.free) return false;
+    if (it == b.free) {
+      t0 = t1 = (uint64_t)wall_clock64();
+      return false;
+    }
+    const bool o = t1 - t0 > (uint64_t)b.ticks;
+    t1 = (uint64_t)wall_clock64();
+    return o;
+  }
+};
+
 // Count n finished producer items on copy (id % NC) (no return value is waited for).
 // NC copies in use (64 or 128: fewer lines to poll against fewer producers per line).
 template <int NC>
@@ -237,7 +258,7 @@ __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u)
                                __HIP_MEMORY_SCOPE_AGENT);
 }
 // Bounded wait (one full wave) until the counter copies sum to at least `target`
-// (wrap-around safe); false if the limit ran out. SLEEP: s_sleep units (64 clocks)
+// (wrap-around safe); false if its time limit ran out. SLEEP: s_sleep units (64 clocks)
 // between polls (longer for waits that overlap weight streaming).
 #ifndef MR_GU_WAIT_SLEEP
 #define MR_GU_WAIT_SLEEP 32  // the down workgroups' wait for the gate/up count
@@ -245,15 +266,17 @@ __device__ __forceinline__ void count(uint32_t* copies, int id, uint32_t n = 1u)
 // Once at most `near` items are missing, polls come every SLEEP_NEAR units instead: the
 // last producers are seen sooner without polling fast through the whole wait.
 template <int SLEEP, int NC, int SLEEP_NEAR = SLEEP>
-__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, uint32_t limit, uint32_t near = 0u) {
+__device__ __forceinline__ bool wait_count(const uint32_t* copies, uint32_t target, const WaitBound& wb,
+                                           uint32_t near = 0u) {
   const int lane = threadIdx.x & 63;
+  WaitTimer tm;
   for (uint32_t it = 0;; ++it) {
     uint32_t c = ld_sc1(copies + kCopyStride * lane);
     if (NC > 64) c += ld_sc1(copies + kCopyStride * (lane + 64));
     const uint32_t sum = wave_sum_u(c);
     const int32_t missing = (int32_t)(target - sum);
     if (missing <= 0) return true;
-    if (it >= limit) return false;
+    if (tm.out(it, wb)) return false;
     if ((uint32_t)missing <= near)
       __builtin_amdgcn_s_sleep(SLEEP_NEAR);
     else
@@ -342,7 +365,7 @@ struct RouteCfg {
   uint32_t n_logits;   // logits published per launch (E, plus extras)
   int E, k;
   uint32_t flags;      // MR_ROUTE_*
-  uint32_t spin_limit;
+  WaitBound wb;
   unsigned long long* trace;  // MR_FUSED_TRACE builds only
 };
 
@@ -637,6 +660,7 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   const uint32_t flag = seq + 1u;
   const int ex = lane < (int)rc.n_logits - rc.E ? rc.E + lane : -1;  // an extra entry of this lane
   float v[kRouteVals];
+  WaitTimer tm;
   for (uint32_t it = 0;; ++it) {
     bool ok = true;
 #pragma unroll
@@ -656,7 +680,7 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
 #endif
       break;
     }
-    if (it >= rc.spin_limit) return false;
+    if (tm.out(it, rc.wb)) return false;
     __builtin_amdgcn_s_sleep(SLEEP);
   }
   RTRACE(1);
@@ -671,7 +695,7 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
     key[j] = (lane + 64 * j < rc.E) ? (v[j] == v[j] ? order_key(v[j] + 0.f) : 1u) : 0u;
   RTRACE(3);
   bool need;
-  const uint32_t T = select_keys<QWEN>(key, nj, rc.k, sel_i, sel_k, tmp, need);
+  (void)select_keys<QWEN>(key, nj, rc.k, sel_i, sel_k, tmp, need);
   if (QWEN && need && !(rc.flags & MR_ROUTE_SOFTMAX_AFTER_TOPK)) {
     const bool pnan = prob_keys(v, rc.E, key);
     prob_select(key, v, rc.E, rc.k, pnan, sel_i, sel_k);

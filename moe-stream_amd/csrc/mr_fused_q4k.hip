@@ -88,7 +88,7 @@ struct Q4Args {
   float alpha, limit;
   int R, ND, NG;
   int gt;  // row tiles per gate/up workgroup
-  uint32_t spin_limit;
+  WaitBound wb;  // time limit of the cross-workgroup waits
   PrefetchRows pf;  // the next layer's router rows (router workgroups read them)
   NormResid nr;     // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
   unsigned long long* trace;
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
   const int nsbH = a.H >> 8, nsbI = a.I >> 8, nGI = a.I >> 4;
   TRACE(0);
   const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
-  const RouteCfg rc{a.fs, (uint32_t)(a.E + a.has_sh), a.E, a.k, a.flags, a.spin_limit, a.trace};
+  const RouteCfg rc{a.fs, (uint32_t)(a.E + a.has_sh), a.E, a.k, a.flags, a.wb, a.trace};
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       TRACE(2);
-      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.spin_limit,
+      if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.wb,
                                                          (uint32_t)a.NG / 4) && lane == 0)
         ok_flag = 0, fail(a.err);
       __syncthreads();
@@ -708,7 +708,16 @@ bool fused_q4k_resident(const mr_layer& L, int n_cu) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, q4_kernel<false>(dn), 256, 0) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, q4_kernel<true>(dn), 256, 0) != hipSuccess)
     return false;
-  return (int64_t)std::min(b0, b1) * n_cu >= grid;
+  if ((int64_t)std::min(b0, b1) * n_cu < grid) return false;
+  // as for the MXFP4 kernel: LDS rounded up to 2 KB per workgroup must fit the CU as well
+  int dev = 0, cu_lds = 0;
+  hipFuncAttributes fa{}, fb{};
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cu_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      hipFuncGetAttributes(&fa, q4_kernel<false>(dn)) != hipSuccess || hipFuncGetAttributes(&fb, q4_kernel<true>(dn)) != hipSuccess)
+    return false;
+  const int64_t wg_lds = (int64_t)((std::max(fa.sharedSizeBytes, fb.sharedSizeBytes) + 2047) & ~(size_t)2047);
+  return wg_lds * ((grid + n_cu - 1) / n_cu) <= (int64_t)cu_lds;
 }
 
 hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, float* y, uint32_t* err,
@@ -736,7 +745,7 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
   const int n_cu = L.ctx->n_cu;
   const Q4Grid g = q4_grid(L, n_cu);
   a.R = (int)g.R, a.ND = (int)g.ND, a.NG = (int)g.NG, a.gt = (int)g.gt;
-  a.spin_limit = L.ctx->spin_limit;
+  a.wb = wait_bound(*L.ctx);
   a.pf = prefetch_plan(L.next);
   a.nr = nr;
   ProfScope ps(K, "fused_layer");

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -89,7 +90,8 @@ struct mr_ctx {
   bool own_stream = false;
   int n_cu = 0;
   int decode_kernel = MR_DECODE_AUTO;
-  uint32_t spin_limit = 1u << 22;  // bounded waits of the fused kernel
+  uint32_t wait_limit_us = 50000;  // time limit of the fused kernels' cross-workgroup waits
+  int wall_khz = 100000;           // rate of the device's constant clock (wall_clock64)
   bool fused_used = false;
   std::string err;
   mr::Scratch scratch;
@@ -173,7 +175,10 @@ hipError_t launch_rms_norm(const Launch& K, const float* h, const float* w, floa
 hipError_t launch_residual_add(const Launch& K, const float* h, const float* m, uint64_t n, float* out);
 hipError_t launch_synth(const Launch& K, int type, void* dst, uint64_t n_blocks, uint64_t seed);
 // Measurement probes (mr_probe.hip).
-hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t* sink);
+hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t depth,
+                             uint32_t* sink);
+hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uint32_t n_tiles, uint32_t n_wg,
+                              uint32_t depth, uint32_t* sink);
 hipError_t launch_probe_empty(const Launch& K, uint32_t n_wg);
 // With `device` current: this device's address of the static scratch array (looked up once
 // per device).
@@ -192,12 +197,24 @@ struct NormResid {
   const float* resid = nullptr;  // [H] residual h (the un-normalised input)
 };
 
+// Time limit of a fused kernel's cross-workgroup waits (mr_fused_common.h): the context's limit in
+// ticks of the device clock; limits below 100 us (a limit forced by a test) consult the clock from
+// the first poll, longer ones after 64 polls.
+struct WaitBound {
+  uint32_t free;   // polls before the clock is consulted
+  uint32_t ticks;  // time limit in clock ticks
+};
+inline WaitBound wait_bound(const mr_ctx& c) {
+  const uint64_t t = (uint64_t)c.wait_limit_us * (uint64_t)c.wall_khz / 1000u;
+  return WaitBound{c.wait_limit_us < 100u ? 0u : 64u, (uint32_t)std::min<uint64_t>(t, 0xFFFFFFFFull)};
+}
+
 // Fused single-launch MXFP4 decode layer (mr_fused.hip).
 constexpr int kSyncErrWord = 96;  // uint32 index of the fused kernel's error word
 bool fused_supported(const mr_layer& L, int n_cu);
 bool fused_resident(const mr_layer& L, int n_cu);      // the whole grid fits the CUs at once
 hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, float* y,
-                        uint32_t* err, uint8_t* img_base, uint32_t spin_limit, int n_cu,
+                        uint32_t* err, uint8_t* img_base, WaitBound wb, int n_cu,
                         const NormResid& nr = NormResid{});
 uint64_t fused_layer_sync_bytes(const mr_layer& L);  // sync block of one layer (its logit count)
 

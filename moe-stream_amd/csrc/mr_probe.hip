@@ -1,27 +1,37 @@
 // mr_probe.hip -- measurement probes for the decode path's ceilings (bench support, not a
 // reference interface): a plain streaming read of a buffer, as fast as the memory system
-// moves bytes with a given number of workgroups, and an empty kernel, whose launches in a
-// graph are the floor of a per-layer kernel boundary.
+// moves bytes with a given number of workgroups and loads in flight, and an empty kernel,
+// whose launches in a graph are the floor of a per-layer kernel boundary.
 #include "mr_device.h"
 #include "mr_internal.h"
 
 namespace mr {
 
-// Workgroup b reads 16-byte pieces b*256 + tid, then + grid*256 ..., four loads in flight per
-// thread, and folds them into one word per workgroup (so no load is dead).
-__global__ __launch_bounds__(256) void k_probe_read(const i32x4* __restrict__ src, uint64_t n16,
+// Workgroup b reads its own contiguous range of the buffer (per16 pieces of 16 bytes), thread
+// t the pieces t, t + 256, ... of that range in batches of D: the D loads of a batch are issued
+// together, then folded (pieces past the range end re-read the range's last piece, a cache
+// hit). The loads are ordinary global loads, so the compiler places every wait for their data.
+// Every piece is folded into one word per workgroup, so no load is dead.
+template <int D>
+__global__ __launch_bounds__(256) void k_probe_read(const i32x4* __restrict__ src, uint64_t n16, uint64_t per16,
                                                     uint32_t* __restrict__ sink) {
-  const uint64_t stride = (uint64_t)gridDim.x * 256;
-  uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t beg = (uint64_t)blockIdx.x * per16;
+  const uint64_t end = min(beg + per16, n16);
   uint32_t acc = 0;
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    const i32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-    acc ^= (uint32_t)(a.x ^ a.y ^ a.z ^ a.w) ^ (uint32_t)(b.x ^ b.y ^ b.z ^ b.w) ^
-           (uint32_t)(c.x ^ c.y ^ c.z ^ c.w) ^ (uint32_t)(d.x ^ d.y ^ d.z ^ d.w);
-  }
-  for (; i < n16; i += stride) {
-    const i32x4 a = src[i];
-    acc ^= (uint32_t)(a.x ^ a.y ^ a.z ^ a.w);
+  if (beg < end) {
+    const uint64_t last = end - 1;
+    const auto* g = (const __attribute__((address_space(1))) i32x4*)(src);
+    for (uint64_t i = beg + threadIdx.x; i < end; i += (uint64_t)D * 256) {
+      i32x4 v[D];
+#pragma unroll
+      for (int j = 0; j < D; ++j) v[j] = g[min(i + (uint64_t)j * 256, last)];
+      __builtin_amdgcn_sched_barrier(0);  // all D loads issue before the first fold
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        const uint32_t f = (uint32_t)(v[j].x ^ v[j].y ^ v[j].z ^ v[j].w);
+        acc ^= i + (uint64_t)j * 256 < end ? f : 0u;  // a select, not a branch
+      }
+    }
   }
   __shared__ uint32_t red[256];
   red[threadIdx.x] = acc;
@@ -33,11 +43,133 @@ __global__ __launch_bounds__(256) void k_probe_read(const i32x4* __restrict__ sr
   }
 }
 
+// The fused MXFP4 kernel's gate/up access pattern: the buffer as rows of rb bytes, tiles of 16
+// adjacent rows; wave w of workgroup b streams tiles 4 (b + k grid) + w over the row in chunks of
+// 204 bytes per row (12 MXFP4 blocks), each chunk as 240-byte 16-byte-aligned row segments, 15
+// per row, lane-contiguous: four 16-byte loads per lane per chunk, D chunks in flight (issued
+// together, then folded). Tiles past n_tiles are not read.
+template <int D>
+__global__ __launch_bounds__(256) void k_probe_tiles(const uint8_t* __restrict__ src, uint32_t rb, uint32_t n_tiles,
+                                                     uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const auto* g = (const __attribute__((address_space(1))) uint8_t*)(src);
+  uint32_t rrb[4], pc16[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int q = it * 64 + lane, row = min(q / 15, 15), pc = min(q - row * 15, 14);
+    rrb[it] = (uint32_t)row * rb;
+    pc16[it] = 16u * (uint32_t)pc;
+  }
+  const int nc = (int)((rb + 203u) / 204u);  // chunks per row
+  uint32_t acc = 0;
+  for (uint32_t t = 4 * blockIdx.x + wave; t < n_tiles; t += 4 * gridDim.x) {
+    const uint64_t base = (uint64_t)t * 16u * rb;
+    const uint32_t a = (uint32_t)(base & 15u);
+    for (int c0 = 0; c0 < nc; c0 += D) {
+      i32x4 v[D][4];
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const uint32_t cb = 204u * (uint32_t)min(c0 + d, nc - 1);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const uint32_t rowa = a + rrb[it];
+          const uint32_t lastr = (rowa + rb - 1u) & ~15u;
+          const uint32_t off = min(((rowa + cb) & ~15u) + pc16[it], lastr);
+          v[d][it] = *(const __attribute__((address_space(1))) i32x4*)(g + (base - a) + off);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // all D chunks issue before the first fold
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int it = 0; it < 4; ++it) acc ^= (uint32_t)(v[d][it].x ^ v[d][it].y ^ v[d][it].z ^ v[d][it].w);
+    }
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+    for (int k = 0; k < 256; ++k) r ^= red[k];
+    sink[blockIdx.x] = r;
+  }
+}
+
+// The same with longer row segments: chunks of S K steps (68 S bytes per row), fetched as
+// 16-byte pieces of npc per row (NL wave loads per chunk), one chunk at a time per wave.
+template <int NL>
+__global__ __launch_bounds__(256) void k_probe_tiles_seg(const uint8_t* __restrict__ src, uint32_t rb, uint32_t n_tiles,
+                                                         uint32_t steps, uint32_t npc, uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const auto* g = (const __attribute__((address_space(1))) uint8_t*)(src);
+  uint32_t rrb[NL], pc16[NL];
+#pragma unroll
+  for (int it = 0; it < NL; ++it) {
+    const int q = it * 64 + lane, row = min(q / (int)npc, 15), pc = min(q - row * (int)npc, (int)npc - 1);
+    rrb[it] = (uint32_t)row * rb;
+    pc16[it] = 16u * (uint32_t)pc;
+  }
+  const uint32_t cbytes = 68u * steps;
+  const int nc = (int)((rb + cbytes - 1u) / cbytes);
+  uint32_t acc = 0;
+  for (uint32_t t = 4 * blockIdx.x + wave; t < n_tiles; t += 4 * gridDim.x) {
+    const uint64_t base = (uint64_t)t * 16u * rb;
+    const uint32_t a = (uint32_t)(base & 15u);
+    for (int c = 0; c < nc; ++c) {
+      i32x4 v[NL];
+#pragma unroll
+      for (int it = 0; it < NL; ++it) {
+        const uint32_t rowa = a + rrb[it];
+        const uint32_t lastr = (rowa + rb - 1u) & ~15u;
+        const uint32_t off = min(((rowa + cbytes * (uint32_t)c) & ~15u) + pc16[it], lastr);
+        v[it] = *(const __attribute__((address_space(1))) i32x4*)(g + (base - a) + off);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int it = 0; it < NL; ++it) acc ^= (uint32_t)(v[it].x ^ v[it].y ^ v[it].z ^ v[it].w);
+    }
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+    for (int k = 0; k < 256; ++k) r ^= red[k];
+    sink[blockIdx.x] = r;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_probe_empty() {}
 
-hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t* sink) {
+hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t depth,
+                             uint32_t* sink) {
   ProfScope ps(K, "probe_read");
-  hipLaunchKernelGGL(k_probe_read, dim3(n_wg), dim3(256), 0, K.s, static_cast<const i32x4*>(src), nbytes / 16, sink);
+  const uint64_t n16 = nbytes / 16;
+  const uint64_t per16 = ((n16 + n_wg - 1) / n_wg + 255) / 256 * 256;  // whole 4 KiB runs per workgroup
+  const auto* s = static_cast<const i32x4*>(src);
+  switch (depth) {
+    case 4: hipLaunchKernelGGL(k_probe_read<4>, dim3(n_wg), dim3(256), 0, K.s, s, n16, per16, sink); break;
+    case 8: hipLaunchKernelGGL(k_probe_read<8>, dim3(n_wg), dim3(256), 0, K.s, s, n16, per16, sink); break;
+    case 16: hipLaunchKernelGGL(k_probe_read<16>, dim3(n_wg), dim3(256), 0, K.s, s, n16, per16, sink); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uint32_t n_tiles, uint32_t n_wg,
+                              uint32_t depth, uint32_t* sink) {
+  ProfScope ps(K, "probe_tiles");
+  const auto* s = static_cast<const uint8_t*>(src);
+  switch (depth) {
+    case 2: hipLaunchKernelGGL(k_probe_tiles<2>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, sink); break;
+    case 4: hipLaunchKernelGGL(k_probe_tiles<4>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, sink); break;
+    case 8: hipLaunchKernelGGL(k_probe_tiles<8>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, sink); break;
+    // depth 0x100 + S: one chunk of S steps at a time (S = 6, 12, 23)
+    case 0x106: hipLaunchKernelGGL(k_probe_tiles_seg<7>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, 6u, 27u, sink); break;
+    case 0x10C: hipLaunchKernelGGL(k_probe_tiles_seg<14>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, 12u, 53u, sink); break;
+    case 0x117: hipLaunchKernelGGL(k_probe_tiles_seg<25>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, 23u, 99u, sink); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

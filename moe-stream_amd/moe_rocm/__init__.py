@@ -26,7 +26,7 @@ ACT_SILU, ACT_SWIGLU_OAI = 0, 1
 DEVICE_NONE = -1
 OPT_DECODE_KERNEL = 1
 OPT_PROFILE = 2
-OPT_SPIN_LIMIT = 3
+OPT_WAIT_LIMIT_US = 3
 DECODE_AUTO, DECODE_VALU, DECODE_FUSED = 0, 1, 2
 
 if not LIB_PATH.exists():
@@ -91,8 +91,9 @@ _SIGS = {
     "mr_moe_forward_residual": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _vp]),
     "mr_moe_forward_batched": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_moe_forward_batched_residual": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _f32, _vp]),
-    "mr_probe_read": (C.c_int, [_vp, _vp, _u64, _u32, _vp]),
+    "mr_probe_read": (C.c_int, [_vp, _vp, _u64, _u32, _u32, _vp]),
     "mr_probe_empty": (C.c_int, [_vp, _u32]),
+    "mr_probe_tiles": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "mr_gguf_close": (None, [_vp]),
@@ -223,8 +224,11 @@ class Context:
         self.check(_lib.mr_graph_end(self.h, C.byref(g)))
         return Graph(self, g.value)
 
-    def probe_read(self, src, nbytes: int, n_workgroups: int, sink) -> None:
-        self.check(_lib.mr_probe_read(self.h, _ptr(src), nbytes, n_workgroups, _ptr(sink)))
+    def probe_read(self, src, nbytes: int, n_workgroups: int, sink, depth: int = 8) -> None:
+        self.check(_lib.mr_probe_read(self.h, _ptr(src), nbytes, n_workgroups, depth, _ptr(sink)))
+
+    def probe_tiles(self, src, row_bytes: int, n_tiles: int, n_workgroups: int, sink, depth: int = 2) -> None:
+        self.check(_lib.mr_probe_tiles(self.h, _ptr(src), row_bytes, n_tiles, n_workgroups, depth, _ptr(sink)))
 
     def probe_empty(self, n_workgroups: int) -> None:
         self.check(_lib.mr_probe_empty(self.h, n_workgroups))

@@ -38,7 +38,7 @@ pub const MR_DECODE_AUTO: c_int = 0;
 pub const MR_DECODE_VALU: c_int = 1;
 pub const MR_DECODE_FUSED: c_int = 2;
 pub const MR_OPT_PROFILE: c_int = 2;
-pub const MR_OPT_SPIN_LIMIT: c_int = 3;
+pub const MR_OPT_WAIT_LIMIT_US: c_int = 3;
 
 pub const MR_STATIC_SCRATCH_BYTES: u64 = 64 << 20;
 
@@ -276,11 +276,4 @@ extern "C" {
         -> c_int;
     pub fn mr_profile_reset(ctx: *mut mr_ctx) -> c_int;
 
-    // ---- synthetic inputs
-    pub fn mr_synth_blocks(ctx: *mut mr_ctx, ggml_type: c_int, dst: *mut c_void, n_blocks: u64, seed: u64) -> c_int;
-
-    // ---- measurement probes
-    pub fn mr_probe_read(ctx: *mut mr_ctx, src: *const c_void, nbytes: u64, n_workgroups: u32, sink: *mut u32)
-        -> c_int;
-    pub fn mr_probe_empty(ctx: *mut mr_ctx, n_workgroups: u32) -> c_int;
 }

@@ -1,5 +1,5 @@
 """C-ABI checks that run without a GPU: the library loads, exports every
-function include/moe_rocm.h declares, and rejects invalid arguments with the
+function include/moe_rocm.h (and the bench-support header moe_rocm_bench.h) declares, and rejects invalid arguments with the
 documented status codes on a host-only context (MR_DEVICE_NONE)."""
 import re
 from pathlib import Path
@@ -11,13 +11,21 @@ import moe_rocm as M
 from moe_rocm import synth as S
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "moe_rocm.h"
+BENCH_HEADER = HEADER.with_name("moe_rocm_bench.h")
 
 
-def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"\b(mr_[a-z0-9_]+)\s*\(", text)
+def declared_functions(headers=(HEADER, BENCH_HEADER)):
+    names = []
+    for h in headers:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"\b(mr_[a-z0-9_]+)\s*\(", text)
     return sorted(set(names))
+
+
+def test_bench_support_stays_out_of_the_drop_in_header():
+    core = declared_functions((HEADER,))
+    for n in ("mr_synth_blocks", "mr_probe_read", "mr_probe_empty", "mr_probe_tiles"):
+        assert n not in core and n in declared_functions((BENCH_HEADER,))
 
 
 def test_header_declares_core_entry_points():

@@ -101,17 +101,63 @@ def test_nan_logits_rank_below_every_number(gpu_ctx, name, kernel):
 def test_probe_read_reads_every_byte(gpu_ctx):
     """mr_probe_read (the plain-stream ceiling of bench.py --probe) folds every 32-bit word of
     the buffer into the per-workgroup sinks: their XOR is the XOR of the whole buffer, for a
-    grid that divides the buffer evenly and one that leaves a ragged tail."""
+    grid that divides the buffer evenly and one that leaves a ragged tail, at every load depth."""
     rng = np.random.default_rng(11)
     data = rng.integers(0, 2**32, size=(1 << 20) // 4 + 4 * 37, dtype=np.uint32)
     want = np.bitwise_xor.reduce(data)
     d = gpu_ctx.to_device(data)
     for n_wg in (64, 548):
-        sink = gpu_ctx.alloc(n_wg * 4)
-        gpu_ctx.probe_read(d, data.nbytes, n_wg, sink)
-        got = np.bitwise_xor.reduce(sink.download(np.uint32))
-        assert got == want, n_wg
-        sink.free()
+        for depth in (4, 8, 16):
+            sink = gpu_ctx.alloc(n_wg * 4)
+            gpu_ctx.probe_read(d, data.nbytes, n_wg, sink, depth=depth)
+            got = np.bitwise_xor.reduce(sink.download(np.uint32))
+            assert got == want, (n_wg, depth)
+            sink.free()
     gpu_ctx.probe_empty(576)
     gpu_ctx.sync()
+    d.free()
+
+
+def _tile_probe_xor(data: np.ndarray, rb: int, n_tiles: int, n_wg: int, steps: int = 3, npc: int = 15) -> int:
+    """XOR of the 16-byte pieces mr_probe_tiles reads (every lane's four pieces of every chunk of
+    every tile its wave streams), restated on the host."""
+    words = data.view(np.uint32)
+    acc = 0
+    lane = np.arange(64)
+    cbytes = 68 * steps
+    nc = (rb + cbytes - 1) // cbytes
+    for it in range((16 * npc + 63) // 64):
+        q = it * 64 + lane
+        row = np.minimum(q // npc, 15)
+        pc = np.minimum(q - row * npc, npc - 1)
+        for t in range(n_tiles):
+            base = t * 16 * rb
+            a = base & 15
+            rowa = a + row * rb
+            lastr = (rowa + rb - 1) & ~15
+            for c in range(nc):
+                off = np.minimum(((rowa + cbytes * c) & ~15) + 16 * pc, lastr) + (base - a)
+                for o in off:
+                    acc ^= int(np.bitwise_xor.reduce(words[o // 4:o // 4 + 4]))
+    return acc
+
+
+def test_probe_tiles_reads_the_gateup_pattern(gpu_ctx):
+    """mr_probe_tiles (the fused kernel's gate/up access pattern, bench.py --probe) folds exactly
+    the pieces that pattern reads, at every depth and for grids smaller and larger than the tile
+    count."""
+    rng = np.random.default_rng(12)
+    rb, n_tiles = 1530, 10
+    data = rng.integers(0, 2**32, size=(n_tiles * 16 * rb + 64) // 4, dtype=np.uint32)
+    want = _tile_probe_xor(data, rb, n_tiles, 0)
+    d = gpu_ctx.to_device(data)
+    for n_wg in (2, 5):
+        for depth in (2, 4, 8, 0x106, 0x10C, 0x117):
+            w = want if depth < 0x100 else _tile_probe_xor(data, rb, n_tiles, 0, depth - 0x100,
+                                                             {6: 27, 12: 53, 23: 99}[depth - 0x100])
+            sink = gpu_ctx.alloc(n_wg * 4)
+            gpu_ctx.probe_tiles(d, rb, n_tiles, n_wg, sink, depth=depth)
+            got = int(np.bitwise_xor.reduce(sink.download(np.uint32)))
+            assert got == w, (n_wg, depth)
+            sink.free()
     d.free()

@@ -510,18 +510,21 @@ def test_fused_graph_replay(gpu_ctx, layers, name):
         b.free()
 
 
-@pytest.mark.parametrize("name", ["C1-gpt-oss", "C3-qwen3-layer0"])
+@pytest.mark.parametrize("name", ["C1-gpt-oss", "C3-qwen3-layer0", "mxfp4-k8", "mxfp4-k4-shared"])
 def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers, name):
     """A tiny spin limit (forced from the host) may make a cross-workgroup wait
-    run out: the kernel still exits, mr_sync reports it, and the next launch
-    with the default limit is correct."""
+    run out: the kernel still exits, mr_sync reports it, and the launches after it
+    with the default limit are correct (their y rows all written again: y is cleared
+    first). The MXFP4 layers with more than four slots (top-8; top-4 + shared) keep a
+    per-row-group counter of down slot groups, which must stay in step through the
+    failed launches."""
     dl, host = get_layer(gpu_ctx, layers, name)
     spec = dl.spec
     x = W.x_tokens(spec, 1, first_token=80)
     dx, dy = gpu_ctx.to_device(x[0]), gpu_ctx.alloc(spec.hidden * 4)
     dl.layer.forward(dx, dy)
     ref = dy.download(np.float32)
-    gpu_ctx.set_option(M.OPT_SPIN_LIMIT, 1)
+    gpu_ctx.set_option(M.OPT_WAIT_LIMIT_US, 1)
     errors = 0
     try:
         for _ in range(5):
@@ -532,10 +535,12 @@ def test_fused_wait_timeout_is_reported_and_recovers(gpu_ctx, layers, name):
                 assert e.status == M.MR_E_LAUNCH and "wait ran out" in e.message
                 errors += 1
     finally:
-        gpu_ctx.set_option(M.OPT_SPIN_LIMIT, 0)
-    dl.layer.forward(dx, dy)
-    gpu_ctx.sync()
-    assert np.array_equal(dy.download(np.float32), ref)
+        gpu_ctx.set_option(M.OPT_WAIT_LIMIT_US, 0)
+    for rep in range(2):
+        gpu_ctx.check(M.lib.mr_dev_zero(gpu_ctx.h, dy.ptr, spec.hidden * 4))
+        dl.layer.forward(dx, dy)
+        gpu_ctx.sync()
+        assert np.array_equal(dy.download(np.float32), ref), rep
     print(f"forced-timeout launches reporting an error: {errors} of 5")
     dx.free(), dy.free()
 

@@ -151,7 +151,7 @@ def test_structs_match_field_by_field():
 def test_constants_have_the_header_values():
     h, r = header_constants(), rust_constants()
     for name in ("MR_OK", "MR_E_INVAL", "MR_E_LAUNCH", "MR_GGML_Q4_K", "MR_GGML_MXFP4", "MR_DECODE_FUSED",
-                 "MR_OPT_SPIN_LIMIT", "MR_STATIC_SCRATCH_BYTES", "MR_ROUTE_NORM_TOPK", "MR_ACT_SWIGLU_OAI"):
+                 "MR_OPT_WAIT_LIMIT_US", "MR_STATIC_SCRATCH_BYTES", "MR_ROUTE_NORM_TOPK", "MR_ACT_SWIGLU_OAI"):
         assert name in h, name
     missing = sorted(set(h) - set(r))
     assert not missing, missing
