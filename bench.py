@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--probe", action="store_true",
                     help="only measure the ceilings: a graph of empty kernels (the kernel-boundary floor) and "
                          "plain streaming reads of the decode layers' byte counts")
+    ap.add_argument("--probe-eager", action="store_true",
+                    help="the plain reads of --probe launched one at a time (512 workgroups, 8 loads in flight), "
+                         "for a kernel trace (rocprofv3 --kernel-trace) of their device durations")
     return ap.parse_args()
 
 
@@ -245,6 +248,58 @@ def probes() -> None:
     pool.free(), sink.free()
     ctx.close()
     print(json.dumps(out), flush=True)
+
+
+def probes_eager() -> None:
+    """The plain reads of probes() launched eagerly, 20 per size over regions of a 1.5 GiB pool (each
+    read from HBM), with 512 workgroups and 8 loads in flight, and the gate/up tile pattern over
+    C2's gate/up bytes: under rocprofv3 --kernel-trace each dispatch's device duration is recorded,
+    without the graph's launch boundary. Prints the sizes in dispatch order."""
+    import moe_rocm as M
+    from moe_rocm import workloads as W
+
+    ctx = M.Context(0)
+    c2 = W.gpt_oss(2, 0)
+    c2_bytes, c3_bytes = c2.weight_bytes_per_token(), W.qwen3_30b(3, 0).weight_bytes_per_token()
+    gu_bytes = c2.top_k * 2 * M.synth.matrix_bytes(c2.ggml_type, c2.inter, c2.hidden)
+    pool_bytes = 1536 << 20
+    pool = ctx.alloc(pool_bytes)
+    ctx.synth_blocks(M.GGML_MXFP4, pool, pool_bytes // 17, 7)
+    sink = ctx.alloc(4 * 4096)
+    sizes = sorted(set([s // 16 * 16 for s in (2_200_000, 4_406_400, 8_812_800, 17_625_600, 106_813_696,
+                                               213_627_392, c2_bytes, gu_bytes, c3_bytes)]))
+    order = []
+    for nbytes in sizes:
+        stride = (nbytes + 4095) // 4096 * 4096
+        n = (pool_bytes - stride) // stride + 1
+        for i in range(20):
+            ctx.probe_read(pool.ptr + (i % n) * stride, nbytes, 512, sink, depth=8)
+        ctx.sync()
+        order.append({"kernel": "probe_read", "nbytes": nbytes, "dispatches": 20})
+    rb = 1530
+    n_tiles = gu_bytes // (16 * rb)
+    stride = (n_tiles * 16 * rb + 4095) // 4096 * 4096
+    for i in range(20):
+        ctx.probe_tiles(pool.ptr + (i % ((pool_bytes - stride) // stride + 1)) * stride, rb, n_tiles, 512, sink, depth=8)
+    ctx.sync()
+    order.append({"kernel": "probe_tiles", "nbytes": n_tiles * 16 * rb, "dispatches": 20})
+    # translations warmed first: a touch of one word per 4 KiB, 64 KiB or 2 MiB of the region,
+    # then the C2 layer's bytes read from it (data still in HBM: the touch reads one line per stride)
+    nbytes = c2_bytes // 16 * 16
+    stride = (nbytes + 4095) // 4096 * 4096
+    n = (pool_bytes - stride) // stride + 1
+    for tstride in (0, 4096, 65536, 2 << 20):
+        for i in range(20):
+            reg = pool.ptr + (i % n) * stride
+            if tstride:
+                ctx.probe_touch(reg, nbytes, tstride, sink)
+            ctx.probe_read(reg, nbytes, 512, sink, depth=8)
+        ctx.sync()
+        order.append({"kernel": "probe_read", "nbytes": nbytes, "dispatches": 20, "touch_stride": tstride,
+                      "interleaved_with": "probe_touch" if tstride else None})
+    pool.free(), sink.free()
+    ctx.close()
+    print(json.dumps({"probe_eager": order, "workgroups": 512, "depth": 8}), flush=True)
 
 
 def trace_decode(a) -> None:
@@ -587,6 +642,9 @@ def main():
         return
     if a.probe:
         probes()
+        return
+    if a.probe_eager:
+        probes_eager()
         return
     if a.trace:
         trace_decode(a)

@@ -219,7 +219,7 @@ int mr_moe_forward_batched_residual(mr_ctx* ctx, const mr_layer* layer, const fl
  * scratch in a static device array of MR_STATIC_SCRATCH_BYTES that every GPU holds for
  * the life of the process (its address is looked up once per device by mr_ctx_create).
  * Calls whose scratch would not fit return MR_E_INVAL with the size in mr_last_error
- * (at the GPT-OSS shape, 64 MiB holds about 600 tokens per call). Every call on one GPU
+ * (at the GPT-OSS shape, 64 MiB holds 631 tokens per call). Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (several contexts or streams,
  * or several host threads) race and must be serialised by the caller. */
 #define MR_STATIC_SCRATCH_BYTES (64ull << 20)

@@ -39,6 +39,11 @@ int mr_probe_empty(mr_ctx* ctx, uint32_t n_workgroups);
  * 4 or 8) chunks in flight; or, with depth 0x100 + S (S = 6, 12 or 23), in chunks of S K steps
  * (68 S bytes per row) one at a time, to see how the segment length moves the rate. One word per
  * workgroup goes to sink. Profile name "probe_tiles". */
+/* One 4-byte read every `stride` bytes (a multiple of 4) of [src, src + nbytes) by 256 workgroups:
+ * caches the range's address translations while reading almost none of its bytes. sink [256] u32
+ * is written only in the rare case a folded word matches a fixed pattern. Profile name
+ * "probe_touch". */
+int mr_probe_touch(mr_ctx* ctx, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink);
 int mr_probe_tiles(mr_ctx* ctx, const void* src, uint32_t row_bytes, uint32_t n_tiles, uint32_t n_workgroups,
                    uint32_t depth, uint32_t* sink);
 

@@ -861,6 +861,17 @@ int mr_probe_tiles(mr_ctx* c, const void* src, uint32_t row_bytes, uint32_t n_ti
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_tiles launch");
 }
 
+int mr_probe_touch(mr_ctx* c, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!src || !sink || nbytes < 4 || stride < 4 || stride % 4 != 0 || misaligned(src, 4))
+    return set_err(c, MR_E_INVAL, "probe_touch: bad arguments");
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  const hipError_t e = mr::launch_probe_touch(c->launch(), src, nbytes - 3, stride, sink);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_touch launch");
+}
+
 int mr_probe_empty(mr_ctx* c, uint32_t n_wg) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   if (n_wg == 0) return set_err(c, MR_E_INVAL, "probe_empty: n_workgroups is 0");

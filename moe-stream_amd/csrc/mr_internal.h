@@ -179,6 +179,7 @@ hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, 
                              uint32_t* sink);
 hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uint32_t n_tiles, uint32_t n_wg,
                               uint32_t depth, uint32_t* sink);
+hipError_t launch_probe_touch(const Launch& K, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink);
 hipError_t launch_probe_empty(const Launch& K, uint32_t n_wg);
 // With `device` current: this device's address of the static scratch array (looked up once
 // per device).

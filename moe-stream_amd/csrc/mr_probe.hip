@@ -139,6 +139,17 @@ __global__ __launch_bounds__(256) void k_probe_tiles_seg(const uint8_t* __restri
   }
 }
 
+// A light touch of a buffer: one 4-byte read every `stride` bytes (for example one per page), so
+// the address translations of the range are cached while almost none of its bytes are read.
+__global__ __launch_bounds__(256) void k_probe_touch(const uint8_t* __restrict__ src, uint64_t nbytes, uint32_t stride,
+                                                     uint32_t* __restrict__ sink) {
+  const uint64_t n = (nbytes + stride - 1) / stride;
+  uint32_t acc = 0;
+  for (uint64_t k = (uint64_t)blockIdx.x * 256 + threadIdx.x; k < n; k += (uint64_t)gridDim.x * 256)
+    acc ^= *reinterpret_cast<const uint32_t*>(src + k * stride);
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;  // keeps the loads; almost never stores
+}
+
 __global__ __launch_bounds__(256) void k_probe_empty() {}
 
 hipError_t launch_probe_read(const Launch& K, const void* src, uint64_t nbytes, uint32_t n_wg, uint32_t depth,
@@ -170,6 +181,12 @@ hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uin
     case 0x117: hipLaunchKernelGGL(k_probe_tiles_seg<25>, dim3(n_wg), dim3(256), 0, K.s, s, rb, n_tiles, 23u, 99u, sink); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_probe_touch(const Launch& K, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink) {
+  ProfScope ps(K, "probe_touch");
+  hipLaunchKernelGGL(k_probe_touch, dim3(256), dim3(256), 0, K.s, static_cast<const uint8_t*>(src), nbytes, stride, sink);
   return hipGetLastError();
 }
 

@@ -94,6 +94,7 @@ _SIGS = {
     "mr_probe_read": (C.c_int, [_vp, _vp, _u64, _u32, _u32, _vp]),
     "mr_probe_empty": (C.c_int, [_vp, _u32]),
     "mr_probe_tiles": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "mr_probe_touch": (C.c_int, [_vp, _vp, _u64, _u32, _vp]),
     "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
     "mr_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "mr_gguf_close": (None, [_vp]),
@@ -229,6 +230,9 @@ class Context:
 
     def probe_tiles(self, src, row_bytes: int, n_tiles: int, n_workgroups: int, sink, depth: int = 2) -> None:
         self.check(_lib.mr_probe_tiles(self.h, _ptr(src), row_bytes, n_tiles, n_workgroups, depth, _ptr(sink)))
+
+    def probe_touch(self, src, nbytes: int, stride: int, sink) -> None:
+        self.check(_lib.mr_probe_touch(self.h, _ptr(src), nbytes, stride, _ptr(sink)))
 
     def probe_empty(self, n_workgroups: int) -> None:
         self.check(_lib.mr_probe_empty(self.h, n_workgroups))
