@@ -11,7 +11,10 @@ Prints ONE JSON line. `value` is tokens/s over the K timed steps (inputs already
 resident in HBM). `roofline` is the dominant kernel's algorithmic bytes per
 launch over its average launch duration, measured with HIP events on the
 library's stream. `cpu_baseline` times the CPU oracle (the C restatement of the
-reference's CPU path) on a bounded sample on this host.
+reference's CPU path) on a bounded sample on this host. `extra_configs` (default run
+only) holds the same measurement, with fewer steps and no CPU leg, for C1, C3 and C4
+(decode) and C5 (batched): value, unit, dominant kernel, its average launch and its
+roofline fraction.
 """
 from __future__ import annotations
 
@@ -50,6 +53,8 @@ def parse():
     ap.add_argument("--no-prefetch-hint", action="store_true",
                     help="do not link each layer to the next (mr_layer_set_next)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="headline only: skip the C1, C3, C4 and C5 rows of extra_configs")
     ap.add_argument("--profile-tokens", type=int, default=16)
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle threads for the CPU baseline (0: every logical core, as the reference's available_parallelism)")
@@ -527,13 +532,11 @@ MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 (the f8f6f4 MFMA with an fp8 B
 MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8
 
 
-def bench_batched(a, ctx, M, W, spec):
+def bench_batched(a, ctx, M, W, spec, config, T, K, Wm, cpu_on):
     """One step = one batched forward of T tokens through one layer (router, top-k, grouped
     gate/up + activation, grouped down, combine). C5: 512 tokens through the Zipf-skewed
     GPT-OSS-shape layer; with --batched T on another config: T tokens through its layer 0
-    (Q4_K layers take the grouped int8-MFMA path)."""
-    T = a.batched or W.CONFIG_TOKENS[5]
-    K, Wm = a.steps if a.steps != 256 else 20, a.warmup
+    (Q4_K layers take the grouped int8-MFMA path). Returns the JSON line's object."""
     dl = W.DeviceLayer(ctx, spec)
     dl.layer.reserve(T)
     H, I = spec.hidden, spec.inter
@@ -583,7 +586,7 @@ def bench_batched(a, ctx, M, W, spec):
         ach = flops[dom] / (avg_ms * 1e-3) / 1e12
         q4 = dom.startswith("grouped_q4k")
         peak = MFMA_INT8_PEAK_TOPS if q4 else MFMA_FP8_PEAK_TFLOPS
-        tr = measured_traffic(a.config) if a.config == 5 and not a.batched else None
+        tr = measured_traffic(config) if config == 5 and T == W.CONFIG_TOKENS[5] else None
         traffic = int(tr["bytes_per_launch"]) if tr and tr.get("kernel") == dom else None
         roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": peak,
                 "unit": "TOP/s" if q4 else "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic,
@@ -593,7 +596,7 @@ def bench_batched(a, ctx, M, W, spec):
                          if q4 else "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this "
                                     "MFMA work")}
     cpu = None
-    if not a.no_cpu_baseline:
+    if cpu_on:
         import oracle  # test infrastructure; used here only as the timed CPU baseline
 
         host = dict(spec=spec)
@@ -612,7 +615,7 @@ def bench_batched(a, ctx, M, W, spec):
                "host": host_cpu(),
                "sample": f"oracle (C restatement of the reference CPU path, {threads} threads) on {ns} of the "
                          f"{T} tokens"}
-    workload = W.CONFIG_NAMES[5] if a.config == 5 else f"{W.CONFIG_NAMES[a.config]}: layer 0, batched {T} tokens"
+    workload = W.CONFIG_NAMES[5] if config == 5 else f"{W.CONFIG_NAMES[config]}: layer 0, batched {T} tokens"
     out = {
         "metric": "expert-FFN batched/prefill tokens/s + MFMA utilisation, GPT-OSS-20B shape",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": Wm,
@@ -620,19 +623,18 @@ def bench_batched(a, ctx, M, W, spec):
         "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if spec.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1)"
                 + ("; Zipf(1.1) router skew)" if spec.zipf_s else ")"),
-        "config": {"workload": workload, "config_id": a.config, "tokens": T, "hidden": H, "inter": I,
+        "config": {"workload": workload, "config_id": config, "tokens": T, "hidden": H, "inter": I,
                    "experts": spec.n_experts, "top_k": spec.top_k, "graph": g is not None},
         "hbm_gbs": round(bytes_step * K / (ms / 1e3) / 1e9, 1),
         "hbm_frac": round(bytes_step * K / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_step": bytes_step,
         "roofline": roof, "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
     if g:
         g.close()
     dx.free(), dy.free()
     dl.close()
-    ctx.close()
+    return out
 
 
 def main():
@@ -660,12 +662,61 @@ def main():
     ctx = M.Context(0)
     kernel_opt = {"auto": M.DECODE_AUTO, "valu": M.DECODE_VALU, "fused": M.DECODE_FUSED}[a.kernel]
     ctx.set_option(M.OPT_DECODE_KERNEL, kernel_opt)
-    specs = W.config_layers(a.config)
     if a.config == 5 or a.batched:
-        bench_batched(a, ctx, M, W, specs[0])
+        T = a.batched or W.CONFIG_TOKENS[5]
+        K = a.steps if a.steps != 256 else 20
+        out = bench_batched(a, ctx, M, W, W.config_layers(a.config)[0], a.config, T, K, a.warmup,
+                            not a.no_cpu_baseline)
+        print(json.dumps(out), flush=True)
+        ctx.close()
         return
+    out, ok = bench_decode(a, ctx, M, W, a.config, a.steps, a.warmup, kernel_opt, not a.no_cpu_baseline,
+                           a.profile_tokens)
+    headline = a.config == 2 and a.batched == 0 and a.decode == "layers" and not a.residual
+    if headline and not a.no_extra_configs:
+        out["extra_configs"] = extra_configs(a, ctx, M, W, kernel_opt)
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    if not ok:
+        log("output check FAILED: the timed pipeline's outputs disagree with the eager VALU path")
+        sys.exit(1)
+
+
+# The other configurations, measured after the headline in the default run: decode tokens
+# through every layer of C1 (8 independent layer copies), C3 and C4, and the C5 batched step,
+# each with fewer timed steps and no CPU leg, so the whole default run stays within minutes.
+EXTRA_STEPS = {1: 512, 3: 256, 4: 256, 5: 20}
+
+
+def extra_configs(a, ctx, M, W, kernel_opt) -> list:
+    rows = []
+    for cfg, K in EXTRA_STEPS.items():
+        t0 = time.perf_counter()
+        if cfg == 5:
+            o = bench_batched(a, ctx, M, W, W.config_layers(5)[0], 5, W.CONFIG_TOKENS[5], K, 3, False)
+            ok = True
+        else:
+            o, ok = bench_decode(a, ctx, M, W, cfg, K, 4, kernel_opt, False, 4)
+        r = o["roofline"] or {}
+        rows.append({"config_id": cfg, "workload": o["config"]["workload"], "metric": o["metric"],
+                     "value": o["value"], "unit": o["unit"], "steps": o["steps"], "ms_per_step": o["ms_per_step"],
+                     "dtype": o["dtype"], "kernel": r.get("kernel"), "avg_launch_us": r.get("avg_launch_us"),
+                     "roofline_bound": r.get("bound"), "achieved": r.get("achieved"), "peak": r.get("peak"),
+                     "roofline_unit": r.get("unit"), "frac": r.get("frac"), "hbm_frac": o.get("hbm_frac"),
+                     "output_check_pass": o["output_check"]["pass"] if "output_check" in o else None,
+                     "seconds": round(time.perf_counter() - t0, 1)})
+        log(f"extra C{cfg}: {o['value']} {o['unit']}, frac {r.get('frac')}, {rows[-1]['seconds']} s")
+        if not ok:
+            log(f"output check FAILED on C{cfg}")
+            sys.exit(1)
+    return rows
+
+
+def bench_decode(a, ctx, M, W, config, K, Wm, kernel_opt, cpu_on, profile_tokens):
+    """Decode tokens through every layer of config `config` (K timed after Wm warmup tokens,
+    one graph per token): the JSON line's object and whether the output check passed."""
+    specs = W.config_layers(config)
     n_layers = len(specs)
-    K, Wm = a.steps, a.warmup
     n_tok = K + Wm
     t0 = time.perf_counter()
     if a.decode == "layers":
@@ -693,7 +744,7 @@ def main():
     wall = time.perf_counter() - wall0
     ctx.sync()  # also reports a fused launch whose cross-workgroup wait ran out
     tok_s = K / (ms / 1e3)
-    if a.config == 1:  # unit: one token through one layer (the 8 instances are independent copies)
+    if config == 1:  # unit: one token through one layer (the 8 instances are independent copies)
         tok_s = K * n_layers / (ms / 1e3)
     y = stack.outputs()
     assert np.all(np.isfinite(y)), "non-finite output"
@@ -710,7 +761,7 @@ def main():
     # live per-kernel timing (HIP events around each launch, eager, same stream)
     ctx.set_option(M.OPT_PROFILE, 1)
     ctx.profile_reset()
-    P = min(a.profile_tokens, n_tok)
+    P = min(profile_tokens, n_tok)
     for t in range(P):
         stack.enqueue_token(t)
     ctx.sync()
@@ -743,18 +794,18 @@ def main():
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     log("kernels: " + ", ".join(f"{k}: n={v[0]} avg={v[1] / v[0] * 1e3:.2f}us" for k, v in kern.items()))
 
-    unit = "layer-tokens/s" if a.config == 1 else "tokens/s"
-    tr = measured_traffic(a.config)
+    unit = "layer-tokens/s" if config == 1 else "tokens/s"
+    tr = measured_traffic(config)
     traffic = None if tr is None or tr.get("kernel") != dom else int(tr["bytes_per_launch"])
 
     cpu = None
-    if not a.no_cpu_baseline:
+    if cpu_on:
         threads = a.cpu_threads or os.cpu_count() or 1
         t0 = time.perf_counter()
         tok_cpu, n_cpu, sec = cpu_baseline(layers, specs, threads)
         log(f"cpu baseline: {tok_cpu:.3f} tok/s ({n_cpu} tokens x {n_layers} layers, {sec:.1f}s of oracle time) "
             f"in {time.perf_counter() - t0:.1f}s")
-        cpu = {"value": round(tok_cpu * n_layers if a.config == 1 else tok_cpu, 3), "unit": unit, "cores": threads,
+        cpu = {"value": round(tok_cpu * n_layers if config == 1 else tok_cpu, 3), "unit": unit, "cores": threads,
                "host": host_cpu(), "kind": "port",
                "sample": f"oracle (C restatement of the reference CPU path; MXFP4 matvec rows and F32 GEMV rows "
                          f"split over {threads} threads, Q4_K dequant single-threaded as in the reference): the same "
@@ -777,9 +828,9 @@ def main():
         # the activation split into 2 int8 terms per 16-element group (int32 sums, f32 scaling)
         "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if s0.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1))",
-        "config": {"workload": W.CONFIG_NAMES[a.config], "config_id": a.config,
+        "config": {"workload": W.CONFIG_NAMES[config], "config_id": config,
                    "layers": n_layers, "tokens": K, "hidden": s0.hidden, "inter": s0.inter,
-                   "experts": [s.n_experts for s in specs][:1] if a.config != 4 else "256..512",
+                   "experts": [s.n_experts for s in specs][:1] if config != 4 else "256..512",
                    "top_k": s0.top_k, "graph": not a.no_graph, "kernel": a.kernel,
                    "next_layer_hint": not a.no_prefetch_hint,
                    "fused_norm_residual": a.residual or a.decode != "layers", "decode": a.decode},
@@ -795,12 +846,8 @@ def main():
         "cpu_baseline": cpu,
         "output_check": check,
     }
-    print(json.dumps(out), flush=True)
     stack.close()
-    ctx.close()
-    if not check["pass"]:
-        log("output check FAILED: the timed pipeline's outputs disagree with the eager VALU path")
-        sys.exit(1)
+    return out, bool(check["pass"])
 
 
 if __name__ == "__main__":

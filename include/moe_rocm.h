@@ -172,8 +172,22 @@ void mr_layer_destroy(mr_layer* layer);
  * HBM. Results do not change. NULL clears the hint; `next` must belong to the
  * same context and stay alive (or be cleared here) while this layer is used. */
 int mr_layer_set_next(mr_layer* layer, const mr_layer* next);
+/* Router logits out of the forward calls themselves: with an array set, every
+ * mr_moe_forward(_residual) and mr_moe_forward_batched(_residual, _noalloc) of
+ * this layer also writes its router logits (x . router row + bias + dummy mask,
+ * the values top-k ranks) as f32 [n_tokens, E] to `logits` (device memory,
+ * 4-byte aligned), in the same launches: the fused decode kernel's router
+ * workgroups store them as they publish them, so no second router GEMV runs.
+ * This is the readback the reference makes after the GPU MoE for router entropy
+ * and routing statistics (layer.rs:879-905). Calls of more than max_tokens tokens
+ * return MR_E_INVAL. NULL clears it. Graphs captured while it is set write to the
+ * array they captured. Results of the calls do not change. */
+int mr_layer_set_logits_out(mr_layer* layer, float* logits, uint32_t max_tokens);
 /* Allocate context scratch for up to max_tokens tokens of this layer's shape
- * (BatchedMoeBuffers::new, metal/mod.rs:1240). Call before graph capture. */
+ * (BatchedMoeBuffers::new, metal/mod.rs:1240). Call before graph capture. A hot-path
+ * call that needs more grows the scratch itself, to at least twice its token capacity;
+ * the old allocation is freed, or, when a graph was captured since it was allocated,
+ * kept until mr_ctx_destroy (the graph still addresses it). */
 int mr_reserve(mr_ctx* ctx, const mr_layer* layer, uint32_t max_tokens);
 
 /* ---- hot path -------------------------------------------------------------- */

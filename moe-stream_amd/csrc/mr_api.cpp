@@ -169,7 +169,13 @@ BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   return p;
 }
 
-int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
+// Scratch grows to cover the largest shape and token count seen. A call that needs more
+// tokens than the scratch holds grows it to at least twice its token capacity (mr_reserve
+// asks for exactly max_tokens), so a token count that creeps up costs O(log T) allocations.
+// The superseded allocation is freed once the stream has drained, unless a graph was
+// captured since it was allocated: such a graph may still address it, so it is kept (with
+// its fused-kernel error word still checked by mr_sync) until mr_ctx_destroy.
+int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T, bool exact = false) {
   mr::Scratch& s = c->scratch;
   uint64_t k = L->d.top_k, E = L->E, I = L->I, H = L->H, Ish = L->Ish;
   if (s.base && T <= s.cap_tokens && k <= s.cap_k && E <= s.cap_e && I <= s.cap_i && H <= s.cap_h &&
@@ -177,19 +183,35 @@ int ensure_scratch(mr_ctx* c, const mr_layer* L, uint64_t T) {
     return MR_OK;
   if (c->capturing)
     return set_err(c, MR_E_INVAL, "scratch too small during graph capture; call mr_reserve first");
-  uint64_t nT = std::max<uint64_t>(T, s.cap_tokens), nk = std::max<uint64_t>(k, s.cap_k);
+  const uint64_t grown = T > s.cap_tokens && !exact ? std::max<uint64_t>(T, 2 * s.cap_tokens) : T;
+  uint64_t nT = std::max<uint64_t>(grown, s.cap_tokens), nk = std::max<uint64_t>(k, s.cap_k);
   uint64_t nE = std::max<uint64_t>(E, s.cap_e), nI = std::max<uint64_t>(I, s.cap_i);
   uint64_t nH = std::max<uint64_t>(H, s.cap_h), nS = std::max<uint64_t>(Ish, s.cap_ish);
   ScratchPlan p = plan_scratch(nT, nk, nE, nI, nH, nS);
-  void* base = nullptr;
-  hipError_t e = hipMalloc(&base, p.total);
-  if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
+  hipError_t e;
   if (s.base) {
-    // a graph captured before may still address the old allocation: keep it
-    c->retired.push_back(s.base);
-    c->retired_err.push_back(s.sync + mr::kSyncErrWord);
-    s.base = nullptr;
+    if (c->captured_since_alloc) {
+      c->retired.push_back(s.base);
+      c->retired_err.push_back(s.sync + mr::kSyncErrWord);
+    } else {
+      // no graph addresses it: drain the stream, keep an unreported wait failure, free it
+      e = hipStreamSynchronize(c->stream);
+      if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+      if (c->fused_used && s.sync) {
+        uint32_t word = 0;
+        e = hipMemcpy(&word, s.sync + mr::kSyncErrWord, 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(c, e, "read fused error word");
+        if (word) c->pending_wait_err = true;
+      }
+      e = hipFree(s.base);
+      if (e != hipSuccess) return hip_fail(c, e, "hipFree(scratch)");
+    }
+    s = mr::Scratch{};
   }
+  void* base = nullptr;
+  e = hipMalloc(&base, p.total);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
+  c->captured_since_alloc = false;
   // sync words and counters must start at zero; later calls keep them balanced
   e = mr::launch_zero(mr::Launch{c->stream, nullptr}, base, p.total);
   if (e != hipSuccess) return hip_fail(c, e, "zero scratch");
@@ -227,6 +249,20 @@ int check_io_align(mr_ctx* c, const float* x, const float* y, const void* idx, c
 int check_layer(mr_ctx* c, const mr_layer* L) {
   if (!L) return set_err(c, MR_E_INVAL, "layer is NULL");
   if (L->ctx != c) return set_err(c, MR_E_INVAL, "layer belongs to another context");
+  return MR_OK;
+}
+
+// The array a T-token forward call of L writes its router logits to: the layer's logits output
+// (mr_layer_set_logits_out) when set, else `own` (scratch). Calls of more tokens than the
+// output holds are refused before anything is launched.
+int logits_dst(mr_ctx* c, const mr_layer* L, uint32_t T, float* own, float** out) {
+  if (!L->logits_out) {
+    *out = own;
+    return MR_OK;
+  }
+  if (T > L->logits_cap)
+    return set_err(c, MR_E_INVAL, "n_tokens %u exceeds the %u tokens of the layer's logits output", T, L->logits_cap);
+  *out = L->logits_out;
   return MR_OK;
 }
 
@@ -372,7 +408,8 @@ int mr_sync(mr_ctx* c) {
   if (c->fused_used && c->scratch.sync) {
     // the current scratch's error word and those of superseded scratch (graphs captured
     // before the scratch grew still write there)
-    bool ran_out = false;
+    bool ran_out = c->pending_wait_err;
+    c->pending_wait_err = false;
     const size_t n_words = 1 + c->retired_err.size();
     for (size_t i = 0; i < n_words; ++i) {
       uint32_t* dev = i == 0 ? c->scratch.sync + mr::kSyncErrWord : c->retired_err[i - 1];
@@ -607,6 +644,15 @@ int mr_layer_create(mr_ctx* c, const mr_layer_desc* d, mr_layer** res) {
   return MR_OK;
 }
 
+int mr_layer_set_logits_out(mr_layer* L, float* logits, uint32_t max_tokens) {
+  if (!L) return set_err(nullptr, MR_E_INVAL, "mr_layer_set_logits_out: layer is NULL");
+  if (logits && max_tokens == 0) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_logits_out: max_tokens is 0");
+  if (misaligned(logits, 4)) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_logits_out: logits must be 4-byte aligned");
+  L->logits_out = logits;
+  L->logits_cap = logits ? max_tokens : 0;
+  return MR_OK;
+}
+
 int mr_layer_set_next(mr_layer* L, const mr_layer* next) {
   if (!L) return set_err(nullptr, MR_E_INVAL, "mr_layer_set_next: layer is NULL");
   if (next && next->ctx != L->ctx) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_next: layers of different contexts");
@@ -634,7 +680,7 @@ int mr_reserve(mr_ctx* c, const mr_layer* L, uint32_t max_tokens) {
   if (max_tokens == 0) return set_err(c, MR_E_INVAL, "max_tokens is 0");
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c))) return rc;
-  return ensure_scratch(c, L, max_tokens);
+  return ensure_scratch(c, L, max_tokens, true);
 }
 
 int mr_router_topk(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, int32_t* idx,
@@ -713,8 +759,9 @@ static int forward_one(mr_ctx* c, const mr_layer* L, const float* x, float* y, c
     e = mr::launch_rms_norm(c->launch(), x, nr.w, nr.eps, 1, L->H, s.xn);
     xin = s.xn, yout = s.ytmp;
   }
-  if (e == hipSuccess) e = mr::launch_router_logits(c->launch(), *L, xin, 1, s.logits);
-  if (e == hipSuccess) e = mr::launch_topk(c->launch(), s.logits, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
+  float* lg = L->logits_out ? L->logits_out : s.logits;
+  if (e == hipSuccess) e = mr::launch_router_logits(c->launch(), *L, xin, 1, lg);
+  if (e == hipSuccess) e = mr::launch_topk(c->launch(), lg, 1, L->E, L->d.top_k, L->d.route_flags, s.idx, s.w);
   if (e == hipSuccess) e = mr::launch_experts_valu(c->launch(), *L, xin, 1, s.idx, s.w, s.act, s.act_sh, yout);
   if (e == hipSuccess && nr.w) e = mr::launch_residual_add(c->launch(), x, s.ytmp, L->H, y);
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "moe forward launch");
@@ -749,7 +796,8 @@ int mr_moe_forward_residual(mr_ctx* c, const mr_layer* L, const float* h, const 
 // layer's type, else the per-token VALU kernels.
 static hipError_t batched_core(mr_ctx* c, const mr_layer* L, const float* x, uint32_t T, float* y) {
   mr::Scratch& s = c->scratch;
-  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, s.logits, s.rpart, s.idx, s.w);
+  float* lg = L->logits_out ? L->logits_out : s.logits;  // T <= logits_cap checked by the caller
+  hipError_t e = mr::launch_router_topk(c->launch(), *L, x, T, lg, s.rpart, s.idx, s.w);
   if (e == hipSuccess) {
     const Batched kind = batched_kind(c, *L);
     if (kind == Batched::grouped_mx)
@@ -770,6 +818,8 @@ int mr_moe_forward_batched(mr_ctx* c, const mr_layer* L, const float* x, uint32_
   if (!x || !y) return set_err(c, MR_E_INVAL, "NULL x or y");
   if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
   if (T == 0) return MR_OK;
+  float* lg;
+  if ((rc = logits_dst(c, L, T, nullptr, &lg))) return rc;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
   const hipError_t e = batched_core(c, L, x, T, y);
@@ -786,6 +836,8 @@ int mr_moe_forward_batched_residual(mr_ctx* c, const mr_layer* L, const float* h
   if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(h_out)) & 15u)
     return set_err(c, MR_E_INVAL, "h, norm_w and h_out must be 16-byte aligned");
   if (T == 0) return MR_OK;
+  float* lg;
+  if ((rc = logits_dst(c, L, T, nullptr, &lg))) return rc;
   if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
   if ((rc = bind(c)) || (rc = ensure_scratch(c, L, T))) return rc;
   mr::Scratch& s = c->scratch;
@@ -803,6 +855,8 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   if ((rc = check_io_align(c, x, y, nullptr, nullptr, nullptr))) return rc;
   if (T == 0) return MR_OK;
   const Batched kind = batched_kind(c, *L);
+  float* lg_out;
+  if ((rc = logits_dst(c, L, T, nullptr, &lg_out))) return rc;
   const BatchedPlan p = plan_batched(T, L->d.top_k, L->E, L->I, L->H, L->Ish, kind);
   if (p.total > mr::kStaticScratchBytes)
     return set_err(c, MR_E_INVAL,
@@ -815,7 +869,7 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
   char* b = static_cast<char*>(c->static_scratch);
   int32_t* idx = reinterpret_cast<int32_t*>(b + p.idx);
   float* w = reinterpret_cast<float*>(b + p.w);
-  float* logits = reinterpret_cast<float*>(b + p.logits);
+  float* logits = lg_out ? lg_out : reinterpret_cast<float*>(b + p.logits);
   float* rpart = reinterpret_cast<float*>(b + p.rpart);
   // no profiling events here: recording them could create events (an allocation)
   const mr::Launch K{c->stream, nullptr};
@@ -891,6 +945,7 @@ int mr_graph_begin(mr_ctx* c) {
   hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamBeginCapture");
   c->capturing = true;
+  c->captured_since_alloc = true;
   return MR_OK;
 }
 

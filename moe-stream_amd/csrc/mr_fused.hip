@@ -69,6 +69,7 @@ struct FusedArgs {
   const float* mask;
   const float* x;
   float* y;
+  float* logits_out;  // router logits [E] of this launch (the layer's logits output) or null
   uint32_t* fs;   // this layer's sync block
   uint32_t* err;  // context error word (read and cleared by mr_sync)
   const uint8_t* sh_gate;  // shared expert matrices (one expert, MXFP4) or null
@@ -365,6 +366,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         if (a.mask) acc = acc + rmask;
       }
       put_logit(a.fs, (uint32_t)(a.E + has_sh), e, seq, acc);
+      if (a.logits_out && e < a.E && lane == 0) a.logits_out[e] = acc;
     }
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, lds_dyn);
@@ -774,6 +776,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
     a.sh_gate_inp = L.d.sh_gate_inp;
   }
   a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
+  a.logits_out = L.logits_out;
   const uint64_t nbH = L.H / 32, nbI = L.I / 32, k = L.d.top_k, ktot = k + (uint64_t)a.has_sh;
   a.dimg = img_base;
   a.dsc = reinterpret_cast<uint32_t*>(img_base + ktot * nbI * kImgBytes);

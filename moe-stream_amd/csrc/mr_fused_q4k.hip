@@ -78,6 +78,7 @@ struct Q4Args {
   const float* sh_gate_inp;
   const float* x;
   float* y;
+  float* logits_out;  // router logits [E] of this launch (the layer's logits output) or null
   uint32_t* fs;     // this layer's sync block
   uint32_t* err;    // context error word
   uint32_t* himg;   // [ktot][I/16][8 words] int8 terms of the down input
@@ -364,6 +365,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         if (a.mask) acc = acc + rmask;
       }
       put_logit(a.fs, (uint32_t)(a.E + a.has_sh), e, seq, acc);
+      if (a.logits_out && e < a.E && lane == 0) a.logits_out[e] = acc;
     }
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, smem);
@@ -737,6 +739,7 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
   a.router_w = L.d.router_w, a.router_b = L.d.router_b, a.mask = L.d.dummy_mask;
   a.sh_gate_inp = L.d.sh_gate_inp;
   a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
+  a.logits_out = L.logits_out;
   a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)L.d.top_k, a.ktot = a.k + a.has_sh;
   const uint64_t nGI = L.I / 16;
   a.himg = reinterpret_cast<uint32_t*>(img_base);

@@ -95,11 +95,14 @@ struct mr_ctx {
   bool fused_used = false;
   std::string err;
   mr::Scratch scratch;
-  // Scratch allocations superseded by a larger one. Graphs captured earlier keep their
-  // addresses, so these stay allocated (and their fused-kernel error words are still
-  // checked by mr_sync) until mr_ctx_destroy.
+  // Scratch allocations superseded by a larger one while a graph captured since their
+  // allocation may still address them: these stay allocated (and their fused-kernel error
+  // words are still checked by mr_sync) until mr_ctx_destroy. A superseded allocation that
+  // no capture has seen is freed at once.
   std::vector<void*> retired;
   std::vector<uint32_t*> retired_err;
+  bool captured_since_alloc = false;  // mr_graph_begin ran since the scratch was allocated
+  bool pending_wait_err = false;      // a freed scratch's error word was set, not yet reported
   // This device's static scratch array (mr_moe_forward_batched_noalloc), resolved at
   // mr_ctx_create; nullptr with static_err set when the lookup failed.
   void* static_scratch = nullptr;
@@ -146,6 +149,8 @@ struct mr_layer {
   int type = 0;
   uint32_t* fused_sync = nullptr;  // device sync block of the fused decode kernel
   const mr_layer* next = nullptr;  // layer run after this one (router prefetch hint) or NULL
+  float* logits_out = nullptr;     // router logits [T, E] of every forward call, or NULL
+  uint32_t logits_cap = 0;         // tokens logits_out holds
   std::vector<mr_pack*> own_packs;  // device objects the layer owns (mr_gguf_layer_create)
   std::vector<void*> own_dev;
 };

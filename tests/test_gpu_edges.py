@@ -55,6 +55,48 @@ def test_graph_survives_scratch_growth(gpu_ctx):
         ctx.close()
 
 
+def _hip_free_bytes() -> int:
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_scratch_growth_without_capture_frees_and_doubles(gpu_ctx):
+    """Token counts that creep up one at a time, with no graph captured: the scratch grows to
+    at least twice its token capacity each time, so only a few allocations are made, and a
+    superseded allocation is freed (device memory in use ends near one scratch, not the sum of
+    every size seen). Results match the oracle throughout."""
+    spec = W.LayerSpec(223, 0, W.GGML_MXFP4, 512, 384, 64, 4, W.ROUTE_SOFTMAX_AFTER_TOPK,
+                       W.ACT_SWIGLU_OAI, True, True)
+    host = W.host_layer(spec)
+    ctx = M.Context(0)  # a fresh context: no graph captured, scratch starts empty
+    dl = W.DeviceLayer(ctx, spec, host=host)
+    n_max = 96
+    try:
+        x = W.x_tokens(spec, n_max, first_token=7)
+        ref, _, _, _ = oracle.layer_from_host(host).forward(x)
+        dxb, dyb = ctx.to_device(x), ctx.alloc(n_max * spec.hidden * 4)
+        ctx.sync()
+        free0 = _hip_free_bytes()
+        for T in range(1, n_max + 1):
+            dl.layer.forward_batched(dxb, T, dyb)
+            if T in (1, 2, 3, 17, 64, n_max):
+                got = dyb.download(np.float32, T * spec.hidden).reshape(T, spec.hidden)
+                assert rel_err(got, ref[:T]) < REL_TOL, T
+        ctx.sync()
+        used = free0 - _hip_free_bytes()
+        # a scratch for 128 tokens of this shape is about 2 MiB (12 KiB per token plus fixed
+        # parts); keeping every superseded allocation would hold over 60 MiB
+        print(f"device memory held after growing to {n_max} tokens: {used / 2**20:.1f} MiB")
+        assert used < 24 << 20, used
+        dxb.free(), dyb.free()
+    finally:
+        dl.close()
+        ctx.close()
+
+
 NAN_SPECS = {
     "mxfp4-E32": W.LayerSpec(221, 0, W.GGML_MXFP4, 512, 256, 32, 4, W.ROUTE_SOFTMAX_AFTER_TOPK,
                              W.ACT_SWIGLU_OAI, True, True),

@@ -669,3 +669,112 @@ def test_fused_routing_ties_take_lowest_index(gpu_ctx, name, pattern):
         gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
         dl.close()
         dx.free(), dy.free()
+
+
+# ---- router logits out of the forward calls (mr_layer_set_logits_out) ------------------
+
+LOGITS_OUT = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k-shared", "C3-qwen3-layer0", "C4-coder-next-layer0",
+              "mxfp4-k4-shared"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", LOGITS_OUT)
+def test_logits_out_matches_router_topk(gpu_ctx, layers, name):
+    """With a logits output set, the decode forward (fused and multi-kernel), its residual form
+    and the batched forward write the router logits the reference reads back after the GPU MoE
+    (layer.rs:879-905): equal to mr_router_topk's on the same input (bitwise on the batched path,
+    which runs that router; within 1e-4 on the fused kernels' own router), and to the oracle's.
+    The outputs y are bitwise the same with and without the logits output; a call of more
+    tokens than the output holds is refused; clearing it stops the writes."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec, H, E = dl.spec, dl.spec.hidden, dl.spec.n_experts
+    L = oracle.layer_from_host(host)
+    T = 20
+    x = W.x_tokens(spec, T, first_token=130)
+    dx, dx1 = gpu_ctx.to_device(x), gpu_ctx.to_device(x[0])
+    dy, dyr = gpu_ctx.alloc(T * H * 4), gpu_ctx.alloc(T * H * 4)
+    dlg, rlg = gpu_ctx.alloc(T * E * 4), gpu_ctx.alloc(T * E * 4)
+    di, dw = gpu_ctx.alloc(T * spec.top_k * 4), gpu_ctx.alloc(T * spec.top_k * 4)
+    nan = np.full(T * E, np.nan, np.float32)
+    try:
+        dl.layer.router_topk(dx, T, di, dw, rlg)
+        router = rlg.download(np.float32).reshape(T, E)
+        _, _, _, olg = L.forward(x)
+        assert np.allclose(router, olg, rtol=1e-4, atol=1e-5 * np.abs(olg).max())
+        for kname, kern in (("fused", M.DECODE_FUSED), ("valu", M.DECODE_VALU)):
+            gpu_ctx.set_option(M.OPT_DECODE_KERNEL, kern)
+            try:
+                dl.layer.forward(dx1, dyr)
+                ref_y = dyr.download(np.float32, H)
+                dl.layer.set_logits_out(dlg, T)
+                dlg.upload(nan)
+                dl.layer.forward(dx1, dy)
+                gpu_ctx.sync()
+                got = dlg.download(np.float32)
+                assert np.array_equal(dy.download(np.float32, H), ref_y), kname
+                assert np.allclose(got[:E], router[0], rtol=1e-4, atol=1e-5 * np.abs(router[0]).max()), kname
+                assert np.all(np.isnan(got[E:])), kname  # one row only
+            finally:
+                dl.layer.set_logits_out(None)
+                gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+        # the batched forward runs mr_router_topk's router: the same bits
+        dl.layer.set_logits_out(dlg, T)
+        dlg.upload(nan)
+        dl.layer.forward_batched(dx, T, dy)
+        gpu_ctx.sync()
+        assert np.array_equal(dlg.download(np.float32).reshape(T, E), router)
+        with pytest.raises(M.MoeRocmError) as ei:
+            dl.layer.set_logits_out(dlg, T - 1)
+            dl.layer.forward_batched(dx, T, dy)
+        assert ei.value.status == M.MR_E_INVAL and "logits output" in ei.value.message
+        # cleared: a forward leaves the array alone
+        dl.layer.set_logits_out(None)
+        dlg.upload(nan)
+        dl.layer.forward(dx1, dy)
+        gpu_ctx.sync()
+        assert np.all(np.isnan(dlg.download(np.float32)))
+    finally:
+        dl.layer.set_logits_out(None)
+        for b in (dx, dx1, dy, dyr, dlg, rlg, di, dw):
+            b.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["C1-gpt-oss", "C3-qwen3-layer0"])
+def test_logits_out_residual_and_graph(gpu_ctx, layers, name):
+    """The residual decode forward writes the logits of rms_norm(h) (the oracle's), and a graph
+    captured with the logits output set writes each replay's logits (new h uploaded between
+    replays, every replay checked)."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec, H, E = dl.spec, dl.spec.hidden, dl.spec.n_experts
+    L = oracle.layer_from_host(host)
+    rng = np.random.default_rng(77 + E)
+    h = (W.x_tokens(spec, 3, first_token=140) * np.float32(2.5)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    eps = 1e-5
+    dn, dh, dout, dlg = gpu_ctx.to_device(nw), gpu_ctx.alloc(H * 4), gpu_ctx.alloc(H * 4), gpu_ctx.alloc(E * 4)
+    dl.layer.reserve(1)
+    dl.layer.set_logits_out(dlg, 1)
+    try:
+        dh.upload(h[0])
+        dl.layer.forward_residual(dh, dn, eps, dout)
+        gpu_ctx.sync()
+        _, _, _, rlg = L.forward_residual(h[0], nw, eps)
+        got = dlg.download(np.float32)
+        assert np.allclose(got, rlg[0], rtol=1e-4, atol=1e-5 * np.abs(rlg).max())
+        gpu_ctx.graph_begin()
+        dl.layer.forward_residual(dh, dn, eps, dout)
+        g = gpu_ctx.graph_end()
+        for t in (1, 2, 0):
+            dh.upload(h[t])
+            dlg.upload(np.full(E, np.nan, np.float32))
+            g.launch()
+            gpu_ctx.sync()
+            _, _, _, rlg = L.forward_residual(h[t], nw, eps)
+            got = dlg.download(np.float32)
+            assert np.allclose(got, rlg[0], rtol=1e-4, atol=1e-5 * np.abs(rlg).max()), t
+        g.close()
+    finally:
+        dl.layer.set_logits_out(None)
+        for b in (dn, dh, dout, dlg):
+            b.free()

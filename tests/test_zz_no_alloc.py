@@ -16,20 +16,26 @@ SPECS = {
     # MXFP4: the grouped MFMA path (pair lists, images, per-pair outputs in the scratch)
     "mxfp4-grouped": W.LayerSpec(230, 0, W.GGML_MXFP4, 512, 384, 20, 10, W.ROUTE_NORM_TOPK, W.ACT_SWIGLU_OAI,
                                  True, True),
-    # Q4_K with a shared expert: the VALU path (activations and shared activations in the scratch)
-    "q4k-shared-valu": W.LayerSpec(231, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
-                                   False, False, sh_inter=256),
+    # Q4_K with a shared expert: the grouped Q4_K MFMA path (pair lists, images, shared rows)
+    "q4k-shared-grouped": W.LayerSpec(231, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                      False, False, sh_inter=256),
     "C1-gpt-oss": W.gpt_oss(1, 0),
 }
-TOKENS = {"mxfp4-grouped": (96, 17), "q4k-shared-valu": (64, 9), "C1-gpt-oss": (200, 33)}
+TOKENS = {"mxfp4-grouped": (96, 17), "q4k-shared-grouped": (64, 9), "C1-gpt-oss": (200, 33)}
+# Layers run with MR_OPT_DECODE_KERNEL = MR_DECODE_VALU, which sends both entry points down the
+# VALU path (activations [T, k, I] and shared activations [T, Ish + 1] in the scratch)
+VALU = {"q4k-shared-valu": "q4k-shared-grouped", "mxfp4-valu": "mxfp4-grouped"}
 
 
-@pytest.mark.parametrize("name", list(SPECS))
+@pytest.mark.parametrize("name", list(SPECS) + list(VALU))
 def test_noalloc_matches_batched(gpu_ctx, name):
-    spec = SPECS[name]
+    base = VALU.get(name, name)
+    spec = SPECS[base]
     dl = W.DeviceLayer(gpu_ctx, spec)
+    if name in VALU:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_VALU)
     try:
-        for call, T in enumerate(TOKENS[name]):  # the second call has fewer tokens
+        for call, T in enumerate(TOKENS[base]):  # the second call has fewer tokens
             x = W.x_tokens(spec, T, first_token=40 * call)
             dx = gpu_ctx.to_device(x)
             dy_ref, dy = gpu_ctx.alloc(T * spec.hidden * 4), gpu_ctx.alloc(T * spec.hidden * 4)
@@ -44,6 +50,7 @@ def test_noalloc_matches_batched(gpu_ctx, name):
             for b in (dx, dy_ref, dy):
                 b.free()
     finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
         dl.close()
 
 
