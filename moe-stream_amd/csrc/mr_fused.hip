@@ -447,8 +447,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const uint8_t* W = (sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e)) +
                          (uint64_t)(pair * 32 + tile * 16) * rb;
       // the epilogue's biases (wave 0, lanes < 32) and shared gate logit, loaded before the stream
-      float gbias = 0.f, ubias = 0.f, zsh = 0.f;
-      if (wave == 0 && has_sh && lane == 0) zsh = get_logit(a.fs, (uint32_t)(a.E + has_sh), a.E);
+      float gbias = 0.f, ubias = 0.f;
+      // every lane, no condition (a load under a lane condition is waited for at once): the
+      // shared gate logit, or the first logit when there is no shared expert (unused then)
+      const float zsh = get_logit(a.fs, (uint32_t)(a.E + has_sh), has_sh ? a.E : 0);
       if (wave == 0 && lane < 32 && !sh) {
         const size_t bi = (size_t)e * a.I + pair * 32 + lane;
         if (a.gate_b) gbias = a.gate_b[bi];

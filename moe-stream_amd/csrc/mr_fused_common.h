@@ -643,6 +643,29 @@ __device__ __forceinline__ void prob_select(const uint32_t (&pkey)[kRouteVals], 
   __builtin_amdgcn_wave_barrier();
 }
 
+// One poll of the published logits: columns 0..NJ-1 (expert lane + 64 j) and the lane's extra
+// entry, every load issued before the first is used. The loads are unconditional, with
+// addresses clamped to a valid entry (absent experts re-read expert E - 1, lanes without an
+// extra entry re-read entry 0): a load under a per-lane condition sits in its own branch, and
+// the wait for it at the join would make the loads one round trip each. True when every
+// entry carries this launch's flag; v gets the logits (-inf past E).
+template <int NJ>
+__device__ __forceinline__ bool poll_logits(const uint64_t* lw, int E, int ex, uint32_t flag, float (&v)[kRouteVals]) {
+  const int lane = threadIdx.x & 63;
+  uint64_t w[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) w[j] = ld64_sc1(lw + min(lane + 64 * j, E - 1));
+  const uint64_t wx = ld64_sc1(lw + (ex >= 0 ? ex : 0));
+  uint32_t bad = (ex >= 0 && (uint32_t)(wx >> 32) != flag) ? 1u : 0u;
+#pragma unroll
+  for (int j = 0; j < kRouteVals; ++j) {
+    const bool in = j < NJ && lane + 64 * j < E;
+    v[j] = in ? __uint_as_float((uint32_t)w[j < NJ ? j : 0]) : -INFINITY;
+    bad |= (in && (uint32_t)(w[j < NJ ? j : 0] >> 32) != flag) ? 1u : 0u;
+  }
+  return __ballot(bad != 0u) == 0ull;
+}
+
 // QWEN: compile in the near-tie check (layers whose flags lack MR_ROUTE_SOFTMAX_AFTER_TOPK rank
 // probabilities); a kernel instantiated without it ranks by logit alone.
 template <int SLEEP = MR_ROUTE_SLEEP, bool QWEN = true>
@@ -662,19 +685,12 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   float v[kRouteVals];
   WaitTimer tm;
   for (uint32_t it = 0;; ++it) {
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j) {
-      const int e = lane + 64 * j;
-      v[j] = -INFINITY;
-      if (j < nj && e < rc.E) {
-        const uint64_t w = ld64_sc1(lw + e);
-        v[j] = __uint_as_float((uint32_t)w);
-        ok = ok && (uint32_t)(w >> 32) == flag;
-      }
-    }
-    if (ex >= 0) ok = ok && (uint32_t)(ld64_sc1(lw + ex) >> 32) == flag;
-    if (__ballot(!ok) == 0ull) {
+    // nj is wave-uniform: one straight-line poll per column count (6 and 7 read 8 columns)
+    const bool ok = nj <= 1   ? poll_logits<1>(lw, rc.E, ex, flag, v)
+                    : nj <= 2 ? poll_logits<2>(lw, rc.E, ex, flag, v)
+                    : nj <= 4 ? poll_logits<4>(lw, rc.E, ex, flag, v)
+                              : poll_logits<8>(lw, rc.E, ex, flag, v);
+    if (ok) {
 #ifdef MR_FUSED_TRACE
       if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 32 + 10] = it;  // polls before the logits were seen
 #endif

@@ -434,8 +434,10 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       const int c0 = kh ? nlo : 0, nu = kh ? nsbH - nlo : nlo;
       const uint8_t* Wr = uniform_ptr(W + (size_t)(urow * 16) * rb + (size_t)c0 * 144);
       // loads used only by the epilogue issue first: the waits for the units never wait for them
-      float zsh = 0.f, gbias = 0.f, ubias = 0.f;
-      if (wave == 0 && a.has_sh && lane == 0) zsh = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.E);
+      float gbias = 0.f, ubias = 0.f;
+      // every lane, no condition (a load under a lane condition is waited for at once): the
+      // shared gate logit, or the first logit when there is no shared expert (unused then)
+      const float zsh = get_logit(a.fs, (uint32_t)(a.E + a.has_sh), a.has_sh ? a.E : 0);
       if (wave == 0 && lane < 16 && !sh) {  // the epilogue's biases
         const size_t bi = (size_t)e * a.I + urow * 16 + lane;
         if (a.gate_b) gbias = a.gate_b[bi];
