@@ -168,7 +168,25 @@ struct UnitPrep {
   i32x4 b[2][2];
   float dsc[2], dm[2];
 };
-__device__ __forceinline__ UnitPrep unit_prep(const uint4& hd, const uint4& w0, const uint4& w1, const UnitLane& ul) {
+// The lane's (d*sc, dmin*m) of sub-blocks g (L = 0) and 4 + g (L = 1) from the unit's header.
+struct UnitScales {
+  float dsc[2], dm[2];
+};
+__device__ __forceinline__ UnitScales unit_scales(const uint4& hd, const UnitLane& ul) {
+  // get_scale_min_k4 (dequant.rs:199-209): j < 4 takes the low 6 bits of bytes j, j+4; j >= 4
+  // the nibbles of byte j+4 and the top 2 bits of bytes j-4, j
+  const float d = __half2float(__ushort_as_half((unsigned short)(hd.x & 0xFFFFu)));
+  const float dmin = __half2float(__ushort_as_half((unsigned short)(hd.x >> 16)));
+  const uint32_t s = ul.sh8;
+  const uint32_t sc0 = __builtin_amdgcn_ubfe(hd.y, s, 6u), m0 = __builtin_amdgcn_ubfe(hd.z, s, 6u);
+  const uint32_t sc1 = __builtin_amdgcn_ubfe(hd.w, s, 4u) | (__builtin_amdgcn_ubfe(hd.y, s + 6u, 2u) << 4);
+  const uint32_t m1 = __builtin_amdgcn_ubfe(hd.w, s + 4u, 4u) | (__builtin_amdgcn_ubfe(hd.z, s + 6u, 2u) << 4);
+  UnitScales u;
+  u.dsc[0] = __fmul_rn(d, (float)sc0), u.dsc[1] = __fmul_rn(d, (float)sc1);
+  u.dm[0] = __fmul_rn(dmin, (float)m0), u.dm[1] = __fmul_rn(dmin, (float)m1);
+  return u;
+}
+__device__ __forceinline__ UnitPrep unit_prep(const UnitScales& u, const uint4& w0, const uint4& w1) {
   UnitPrep p;
 #pragma unroll
   for (int L = 0; L < 2; ++L) {
@@ -179,18 +197,12 @@ __device__ __forceinline__ UnitPrep unit_prep(const uint4& hd, const uint4& w0, 
       p.b[L][hi] = i32x4{(int)((w.x >> s) & 0x0F0F0F0Fu), (int)((w.y >> s) & 0x0F0F0F0Fu),
                          (int)((w.z >> s) & 0x0F0F0F0Fu), (int)((w.w >> s) & 0x0F0F0F0Fu)};
     }
+    p.dsc[L] = u.dsc[L], p.dm[L] = u.dm[L];
   }
-  // get_scale_min_k4 (dequant.rs:199-209): j < 4 takes the low 6 bits of bytes j, j+4; j >= 4
-  // the nibbles of byte j+4 and the top 2 bits of bytes j-4, j
-  const float d = __half2float(__ushort_as_half((unsigned short)(hd.x & 0xFFFFu)));
-  const float dmin = __half2float(__ushort_as_half((unsigned short)(hd.x >> 16)));
-  const uint32_t s = ul.sh8;
-  const uint32_t sc0 = __builtin_amdgcn_ubfe(hd.y, s, 6u), m0 = __builtin_amdgcn_ubfe(hd.z, s, 6u);
-  const uint32_t sc1 = __builtin_amdgcn_ubfe(hd.w, s, 4u) | (__builtin_amdgcn_ubfe(hd.y, s + 6u, 2u) << 4);
-  const uint32_t m1 = __builtin_amdgcn_ubfe(hd.w, s + 4u, 4u) | (__builtin_amdgcn_ubfe(hd.z, s + 6u, 2u) << 4);
-  p.dsc[0] = __fmul_rn(d, (float)sc0), p.dsc[1] = __fmul_rn(d, (float)sc1);
-  p.dm[0] = __fmul_rn(dmin, (float)m0), p.dm[1] = __fmul_rn(dmin, (float)m1);
   return p;
+}
+__device__ __forceinline__ UnitPrep unit_prep(const uint4& hd, const uint4& w0, const uint4& w1, const UnitLane& ul) {
+  return unit_prep(unit_scales(hd, ul), w0, w1);
 }
 
 // One unit: this lane's share of row i's dot product (lanes i, i+16, i+32, i+48 hold the four
@@ -559,6 +571,17 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       float ybias = 0.f;  // this row's routed bias terms (layer.rs:1417-1444)
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
+      // every unit's sub-block scales are decoded while the gate/up results are awaited (the
+      // weights land long before the count completes; the scales take the header's registers)
+      [[maybe_unused]] UnitScales US[STREAM ? 1 : kQ4RingD];
+      if constexpr (!STREAM) {
+#pragma unroll
+        for (int r = 0; r < kQ4RingD; ++r) {
+          US[r] = unit_scales(R.hd[r], ul);
+          // materialised here: the compiler would otherwise sink the decode to its use
+          asm volatile("" : "+v"(US[r].dsc[0]), "+v"(US[r].dsc[1]), "+v"(US[r].dm[0]), "+v"(US[r].dm[1]));
+        }
+      }
       TRACE(2);
       if (wave == 0 && !wait_count<MR_GU_WAIT_SLEEP, 128, 4>(a.fs + FS_GU, (seq + 1u) * (uint32_t)a.NG, a.wb,
                                                          (uint32_t)a.NG / 4) && lane == 0)
@@ -594,7 +617,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
             const UnitOps cur = op;
             if (r + 1 < kQ4RingD)
               op = unit_ops(ul, (uint32_t)(sj[(r + 1) / DN] * nGI + ((r + 1) % DN) * 16), smem);
-            acc += unit_dot(R.hd[r], R.w0[r], R.w1[r], ul, cur);
+            acc += unit_dot(unit_prep(US[r], R.w0[r], R.w1[r]), cur);
             if (c == DN - 1) {  // the slot's last super-block: lanes 0-15 store its rows (repeated
                                 // slots and the other lanes store to this wave's spare row)
               acc = row_total(acc);
