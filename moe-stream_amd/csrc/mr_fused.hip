@@ -336,16 +336,16 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const float rbias = (e < a.E && a.router_b) ? a.router_b[e] : 0.f;
       const float rmask = (e < a.E && a.mask) ? a.mask[e] : 0.f;
       f32x4 xv[kRouterVec], wv[kRouterVec];  // every load issued before the first use
+      const float* wr = w ? w : a.x;          // no row (no shared gate input): a zero logit
 #pragma unroll
       for (int j = 0; j < kRouterVec; ++j) {
         const int c = (lane + 64 * j) * 4;
-        const bool in = c < a.H && w != nullptr;
-        xv[j] = in ? *reinterpret_cast<const f32x4*>(a.x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-        wv[j] = in ? *reinterpret_cast<const f32x4*>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        xv[j] = ld4_or0(a.x, c, a.H);
+        wv[j] = ld4_or0(wr, w ? c : a.H, a.H);
       }
       if (NORM) {  // x = rms_norm(h)
         f32x4 nv[kRouterVec];
-        load_lanes4(a.nr.w, a.H, nv);
+        load_lanes4_all(a.nr.w, a.H, nv);
         const float inv = rms_inv(xv, a.H, a.nr.eps);
 #pragma unroll
         for (int j = 0; j < kRouterVec; ++j)
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       }
       if (NORM) {  // x = rms_norm(h): each wave derives inv the way the router waves do
         f32x4 hv[kRouterVec];
-        load_lanes4(a.x, a.H, hv);
+        load_lanes4_all(a.x, a.H, hv);
         f32x2 nlo[kRounds], nhi[kRounds];
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {

@@ -309,6 +309,16 @@ __device__ __forceinline__ float rms_inv(const f32x4 (&xv)[NV], int H, float eps
   s = wave_sum(s);  // the same bits in every lane
   return 1.f / sqrtf(s / (float)H + eps);
 }
+// An in-bounds float4 load whatever the index (the index clamped to the last float4), zero
+// selected afterwards for indices past n (a multiple of 4). A load under a per-lane condition
+// is compiled into a branch of its own, and the wait at the branch's end can make a run of
+// such loads one memory round trip each; these issue together. Where loads are off the
+// critical path the conditional form can be the faster one (it adds fewer requests while the
+// critical ones are in flight): the choice is measured per use.
+__device__ __forceinline__ f32x4 ld4_or0(const float* v, int c, int n) {
+  const f32x4 t = *reinterpret_cast<const f32x4*>(v + min(c, n - 4));
+  return c < n ? t : f32x4{0.f, 0.f, 0.f, 0.f};
+}
 // A wave's lane-strided float4s of v (zero past H).
 template <int NV>
 __device__ __forceinline__ void load_lanes4(const float* v, int H, f32x4 (&out)[NV]) {
@@ -318,6 +328,13 @@ __device__ __forceinline__ void load_lanes4(const float* v, int H, f32x4 (&out)[
     const int c = (lane + 64 * j) * 4;
     out[j] = c < H ? *reinterpret_cast<const f32x4*>(v + c) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
+}
+// The same, every load unconditional (ld4_or0).
+template <int NV>
+__device__ __forceinline__ void load_lanes4_all(const float* v, int H, f32x4 (&out)[NV]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) out[j] = ld4_or0(v, (lane + 64 * j) * 4, H);
 }
 __device__ __forceinline__ float norm1(float x, float inv, float w) { return (x * inv) * w; }
 
