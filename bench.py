@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--trace", action="store_true",
                     help="only trace one fused MXFP4 decode launch (layer 5 of a token, --config 1 or 2) with the "
                          "library built by `python moe-stream_amd/moe_rocm/build.py --trace`: phase times per role")
+    ap.add_argument("--trace-graph", action="store_true",
+                    help="with --trace: trace two consecutive layers inside a replayed token graph (the timed "
+                         "pipeline's conditions), and the gap between them")
     ap.add_argument("--probe", action="store_true",
                     help="only measure the ceilings: a graph of empty kernels (the kernel-boundary floor) and "
                          "plain streaming reads of the decode layers' byte counts")
@@ -326,7 +329,10 @@ def trace_decode(a) -> None:
     M._lib.mr_debug_fused_trace.argtypes = [C.c_void_p]
     ctx = M.Context(0)
     specs = W.config_layers(a.config)
-    stack = W.DecodeStack(ctx, specs, residual=a.residual)
+    if a.decode == "chain":
+        stack = W.ChainStack(ctx, specs)
+    else:
+        stack = W.DecodeStack(ctx, specs, residual=a.residual)
     stack.load(stack.inputs(8))
     for t in range(6):
         stack.enqueue_token(t)
@@ -338,20 +344,47 @@ def trace_decode(a) -> None:
         has_sh = 1 if s0.sh_inter else 0
         R, ND, NG = (s0.n_experts + has_sh + 3) // 4, s0.hidden // 16, (s0.top_k + has_sh) * (s0.inter // 16)
     buf = ctx.zeros((1024 * 32,), dtype=np.uint64)
+    prev = ctx.zeros((1024 * 32,), dtype=np.uint64)  # --trace-graph: the layer before
     def launch(l):
-        if a.residual:
+        if a.decode == "chain":
+            h = stack.h_ptr(6)
+            stack.layers[l].layer.forward_residual(h, stack.d_nw.ptr + l * stack.H * 4, stack.eps, h)
+        elif a.residual:
             stack.layers[l].layer.forward_residual(stack.x_ptr(6, l), stack.d_nw.ptr + l * stack.H * 4, stack.eps,
                                                    stack.y_ptr(l))
         else:
             stack.layers[l].layer.forward(stack.x_ptr(6, l), stack.y_ptr(l))
 
-    for l in range(li):
-        launch(l)
-    ctx.sync()
-    M._lib.mr_debug_fused_trace(buf.ptr)
-    launch(li)
-    ctx.sync()
-    M._lib.mr_debug_fused_trace(None)
+    gap_us = None
+    if a.trace_graph:
+        # one token through every layer in a graph, as the timed pipeline runs it; the trace
+        # pointer is set while layers li-1 and li are captured (their launch arguments keep it)
+        li = max(li, 1)
+        ctx.sync()
+        ctx.graph_begin()
+        for l in range(len(specs)):
+            M._lib.mr_debug_fused_trace(prev.ptr if l == li - 1 else (buf.ptr if l == li else None))
+            launch(l)
+        M._lib.mr_debug_fused_trace(None)
+        g = ctx.graph_end()
+        for _ in range(4):
+            g.launch()
+        ctx.sync()
+        g.close()
+        tp = prev.download(np.uint64).reshape(1024, 32).astype(np.int64)
+        tb = buf.download(np.uint64).reshape(1024, 32).astype(np.int64)
+        np_ = int(np.count_nonzero(tp[:, 0]))
+        nb = int(np.count_nonzero(tb[:, 0]))
+        gap_us = {"previous_layer_last_exit_to_first_start": round(float(tb[:nb, 0].min() - tp[:np_, 5].max()) / 100.0, 2),
+                  "previous_layer_us": round(float(tp[:np_, 5].max() - tp[:np_, 0].min()) / 100.0, 2)}
+    else:
+        for l in range(li):
+            launch(l)
+        ctx.sync()
+        M._lib.mr_debug_fused_trace(buf.ptr)
+        launch(li)
+        ctx.sync()
+        M._lib.mr_debug_fused_trace(None)
     tr = buf.download(np.uint64).reshape(1024, 32).astype(np.int64)
     grid = int(np.count_nonzero(tr[:, 0]))
     us = (tr[:grid] - tr[:grid, 0].min()) / 100.0
@@ -402,11 +435,14 @@ def trace_decode(a) -> None:
         key = f"{sum(role[c] == 'gateup' for c in co)} gateup + {sum(role[c] == 'down' for c in co)} down"
         groups.setdefault(key, []).append(us[b, 3] - us[b, 2])
     out = {"trace": W.CONFIG_NAMES[a.config], "layer": li, "workgroups": grid, "cus": len(by_cu),
+           "mode": ("graph, " if a.trace_graph else "eager, ") + ("chain" if a.decode == "chain" else
+                                                                   "residual" if a.residual else "layers"),
+           "gap": gap_us,
            "kernel_us": round(float(us[:, 5].max()), 2), "phases_us": phases,
            "gateup_stream_us_by_cu_load": {k: {"workgroups": len(v), "median": round(float(np.median(v)), 2),
                                                "max": round(float(max(v)), 2)} for k, v in sorted(groups.items())}}
     print(json.dumps(out), flush=True)
-    buf.free()
+    buf.free(), prev.free()
     stack.close()
     ctx.close()
 

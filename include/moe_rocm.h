@@ -172,6 +172,14 @@ void mr_layer_destroy(mr_layer* layer);
  * HBM. Results do not change. NULL clears the hint; `next` must belong to the
  * same context and stay alive (or be cleared here) while this layer is used. */
 int mr_layer_set_next(mr_layer* layer, const mr_layer* next);
+/* Prefetch hint for the fused residual decode (no reference counterpart): the
+ * norm weights the caller passes to this layer's mr_moe_forward_residual
+ * (the post-attention norm, layer.rs:462-463). The layer whose next layer
+ * (mr_layer_set_next) this is reads them into the caches while it runs, as it
+ * does the router rows. Results do not change. NULL clears it; norm_w must stay
+ * valid while set (device f32 [H], 16-byte aligned). mr_gguf_layer_create sets
+ * it to the norm weights the layer owns. */
+int mr_layer_set_norm(mr_layer* layer, const float* norm_w);
 /* Router logits out of the forward calls themselves: with an array set, every
  * mr_moe_forward(_residual) and mr_moe_forward_batched(_residual, _noalloc) of
  * this layer also writes its router logits (x . router row + bias + dummy mask,

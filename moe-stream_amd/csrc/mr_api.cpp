@@ -653,6 +653,13 @@ int mr_layer_set_logits_out(mr_layer* L, float* logits, uint32_t max_tokens) {
   return MR_OK;
 }
 
+int mr_layer_set_norm(mr_layer* L, const float* norm_w) {
+  if (!L) return set_err(nullptr, MR_E_INVAL, "mr_layer_set_norm: layer is NULL");
+  if (misaligned(norm_w, 16)) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_norm: norm_w must be 16-byte aligned");
+  L->norm_w = norm_w;
+  return MR_OK;
+}
+
 int mr_layer_set_next(mr_layer* L, const mr_layer* next) {
   if (!L) return set_err(nullptr, MR_E_INVAL, "mr_layer_set_next: layer is NULL");
   if (next && next->ctx != L->ctx) return set_err(L->ctx, MR_E_INVAL, "mr_layer_set_next: layers of different contexts");

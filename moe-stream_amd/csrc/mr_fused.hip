@@ -91,6 +91,7 @@ struct FusedArgs {
   int perm_nc;  // CU count of the role permutation (role_index), 0: identity
   uint32_t lds_img_bytes;     // dynamic LDS: image bytes, then 4-byte scales
   PrefetchRows pf;            // the next layer's router rows (router workgroups read them)
+  const float* pf_nw;         // the next layer's norm weights (mr_layer_set_norm) or null
   NormResid nr;               // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
   unsigned long long* trace;  // MR_FUSED_TRACE builds only: [grid][16] timestamps
 };
@@ -370,6 +371,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     }
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, lds_dyn);
+    prefetch_norm(a.pf_nw, a.H, bid, lds_dyn);
   } else if (bid >= a.R + a.ND && bid < a.R + a.ND + a.NG) {
     // ------------------------------------------------------------- gate/up
     const int gid = bid - a.R - a.ND;
@@ -791,6 +793,7 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.dn_delay = dn_delay_rounds(L);
   a.wb = wb;
   a.pf = prefetch_plan(L.next);
+  a.pf_nw = L.next && L.next->H == L.H ? L.next->norm_w : nullptr;
   a.nr = nr;
   a.lds_img_bytes = (uint32_t)fused_lds_img_bytes(L);
   const size_t lds = fused_lds_bytes(L);

@@ -364,6 +364,18 @@ __device__ __forceinline__ void prefetch_rows(const PrefetchRows& p, int bid, in
   }
   vm_drain();  // the loads complete before this workgroup's LDS is released
 }
+// The next layer's norm weights (mr_layer_set_norm), which every router and gate/up workgroup
+// of that layer reads: each of the first eight router workgroups (one per XCD, workgroups being
+// dealt to the XCDs in turn) reads all H of them, its four waves a quarter each.
+__device__ __forceinline__ void prefetch_norm(const float* nw, int H, int bid, uint8_t* lds) {
+  if (!nw || bid >= 8) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int j = wave; j * 256 < H; j += 4) {
+    const int c = min(j * 256 + lane * 4, H - 4);
+    __builtin_amdgcn_global_load_lds(nw + c, lds + wave * 1024, 16, 0, 0);
+  }
+  vm_drain();
+}
 // Host side: the plan for the hint set with mr_layer_set_next (no prefetch without one).
 inline PrefetchRows prefetch_plan(const mr_layer* n) {
   PrefetchRows p{nullptr, nullptr, 0, 0, 0};

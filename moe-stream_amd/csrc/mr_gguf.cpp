@@ -568,6 +568,7 @@ extern "C" int mr_gguf_layer_create(mr_ctx* ctx, const mr_gguf* g, uint32_t l, c
   mr_layer* L = nullptr;
   if ((rc = mr_layer_create(ctx, &d, &L))) return cleanup(rc);
   mr::layer_adopt(L, packs.data(), packs.size(), owned.data(), owned.size());
+  L->norm_w = nw;  // owned by the layer: the previous layer may prefetch it
   if (norm_w) *norm_w = nw;
   *out = L;
   return MR_OK;

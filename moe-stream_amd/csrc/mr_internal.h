@@ -149,6 +149,7 @@ struct mr_layer {
   int type = 0;
   uint32_t* fused_sync = nullptr;  // device sync block of the fused decode kernel
   const mr_layer* next = nullptr;  // layer run after this one (router prefetch hint) or NULL
+  const float* norm_w = nullptr;   // norm weights of this layer's residual forwards (prefetch hint) or NULL
   float* logits_out = nullptr;     // router logits [T, E] of every forward call, or NULL
   uint32_t logits_cap = 0;         // tokens logits_out holds
   std::vector<mr_pack*> own_packs;  // device objects the layer owns (mr_gguf_layer_create)

@@ -83,6 +83,7 @@ _SIGS = {
     "mr_layer_create": (C.c_int, [_vp, C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "mr_layer_destroy": (None, [_vp]),
     "mr_layer_set_next": (C.c_int, [_vp, _vp]),
+    "mr_layer_set_norm": (C.c_int, [_vp, _vp]),
     "mr_layer_set_logits_out": (C.c_int, [_vp, _vp, C.c_uint32]),
     "mr_reserve": (C.c_int, [_vp, _vp, _u32]),
     "mr_router_topk": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
@@ -355,6 +356,11 @@ class MoeLayer:
         """Prefetch hint: `nxt` runs after this layer (mr_layer_set_next); results do not change."""
         self.ctx.check(_lib.mr_layer_set_next(self.h, nxt.h if nxt is not None else None))
         self._next = nxt  # keeps the next layer alive while this one may prefetch it
+
+    def set_norm(self, norm_w) -> None:
+        """Prefetch hint: the norm weights (device buffer or address) passed to this layer's
+        residual forwards (mr_layer_set_norm); results do not change."""
+        self.ctx.check(_lib.mr_layer_set_norm(self.h, _ptr(norm_w)))
 
     def set_logits_out(self, logits, max_tokens: int = 1) -> None:
         """Forward calls also write their router logits [T, E] f32 to the device buffer

@@ -295,6 +295,9 @@ class DecodeStack:
         self.eps = 1e-5
         self.norm_w = norm_weights(n, self.H) if residual else None
         self.d_nw = ctx.to_device(self.norm_w) if residual else None
+        if residual and prefetch_hint:  # each layer's norm weights, read ahead by the layer before
+            for li, dl in enumerate(self.layers):
+                dl.layer.set_norm(self.d_nw.ptr + li * self.H * 4)
         self.d_x = self.d_y = None
         self.graphs: list = []
 

@@ -161,6 +161,7 @@ extern "C" {
     pub fn mr_layer_create(ctx: *mut mr_ctx, desc: *const mr_layer_desc, out: *mut *mut mr_layer) -> c_int;
     pub fn mr_layer_destroy(layer: *mut mr_layer);
     pub fn mr_layer_set_next(layer: *mut mr_layer, next: *const mr_layer) -> c_int;
+    pub fn mr_layer_set_norm(layer: *mut mr_layer, norm_w: *const f32) -> c_int;
     pub fn mr_layer_set_logits_out(layer: *mut mr_layer, logits: *mut f32, max_tokens: u32) -> c_int;
     pub fn mr_reserve(ctx: *mut mr_ctx, layer: *const mr_layer, max_tokens: u32) -> c_int;
 

@@ -778,3 +778,41 @@ def test_logits_out_residual_and_graph(gpu_ctx, layers, name):
         dl.layer.set_logits_out(None)
         for b in (dn, dh, dout, dlg):
             b.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pair", [("C1-gpt-oss", "C1-gpt-oss"), ("tiny-mxfp4", "tiny-q4k-shared"),
+                                  ("C3-qwen3-layer0", "C4-coder-next-layer0")], ids=lambda p: f"{p[0]}->{p[1]}")
+def test_norm_hint_keeps_results(gpu_ctx, layers, pair):
+    """mr_layer_set_norm only lets the layer before prefetch the norm weights: both layers'
+    residual outputs are bitwise the same with and without the hints (next layer and norm
+    weights), and clearing them works."""
+    a, b = (get_layer(gpu_ctx, layers, n)[0] for n in pair)
+    if a.spec.hidden != b.spec.hidden:
+        pytest.skip("the chained layers share the hidden size")
+    H = a.spec.hidden
+    rng = np.random.default_rng(17 + H)
+    nw = (1.0 + 0.1 * rng.standard_normal((2, H))).astype(np.float32)
+    dnw = gpu_ctx.to_device(nw)
+    h0 = (W.x_tokens(a.spec, 1, first_token=150)[0] * np.float32(2.0)).astype(np.float32)
+    dh = gpu_ctx.alloc(H * 4)
+
+    def run():
+        dh.upload(h0)
+        a.layer.forward_residual(dh, dnw.ptr, 1e-5, dh)
+        b.layer.forward_residual(dh, dnw.ptr + H * 4, 1e-5, dh)
+        gpu_ctx.sync()
+        return dh.download(np.float32)
+
+    ref = run()
+    try:
+        a.layer.set_next(b.layer)
+        b.layer.set_norm(dnw.ptr + H * 4)
+        a.layer.set_norm(dnw.ptr)
+        for _ in range(3):
+            assert np.array_equal(run(), ref)
+    finally:
+        a.layer.set_next(None)
+        a.layer.set_norm(None), b.layer.set_norm(None)
+    assert np.array_equal(run(), ref)
+    dnw.free(), dh.free()
