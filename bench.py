@@ -629,7 +629,7 @@ def bench_batched(a, ctx, M, W, spec, config, T, K, Wm, cpu_on):
                 "traffic_source": "profiles/traffic.json (rocprofv3 --pmc)" if traffic else None,
                 "flops_per_launch": flops[dom], "avg_launch_us": round(avg_ms * 1e3, 2),
                 "note": ("GEMM ops of the layer; the 2-term int8 activation split issues 2x this MFMA work"
-                         if q4 else "GEMM flops of the layer; the 4-term e4m3 activation split issues 4x this "
+                         if q4 else "GEMM flops of the layer; the 3-term e4m3 activation split issues 3x this "
                                     "MFMA work")}
     cpu = None
     if cpu_on:
@@ -656,7 +656,7 @@ def bench_batched(a, ctx, M, W, spec, config, T, K, Wm, cpu_on):
         "metric": "expert-FFN batched/prefill tokens/s + MFMA utilisation, GPT-OSS-20B shape",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(ms / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "mxfp4-weights/e4m3x4-act/f32-acc" if spec.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
+        "dtype": "mxfp4-weights/e4m3x3-act/f32-acc" if spec.mxfp4 else "q4_k-weights/int8x2-act/i32-f32-acc",
         "data": "synthetic (seeded SplitMix64 weights generated on the GPU; x ~ N(0,1)"
                 + ("; Zipf(1.1) router skew)" if spec.zipf_s else ")"),
         "config": {"workload": workload, "config_id": config, "tokens": T, "hidden": H, "inter": I,

@@ -157,12 +157,14 @@ struct GroupedArgs {
 // Grouped GEMM work item: (expert e, row tile, 32-pair tile); 4 waves. A wave owns kGT
 // 16-row A tiles of one matrix (gate/up: waves 0-1 gate, 2-3 up, the same 96 rows; down:
 // 4 x 48 = 192 rows) and the tile's 32 pairs as 2 groups of 16.
-// One MFMA covers 16 rows x 1 weight block x 16 pairs, with the 4 e4m3 terms of the pairs'
-// activation block along K: K group j of the MFMA is term j, so the A operand is the
-// weight block repeated in every K group (each with the block's scale byte) and B's
-// group j is term j of the 16 pairs (with term j's scale byte). D then holds the term-summed
-// dot product of row x pair: no term columns to add afterwards, 16 pairs per MFMA, and a
-// wave keeps kGT x 2 accumulator tiles.
+// The MFMAs take the first kGemmTerms = 3 e4m3 terms of the pairs' activation split (the
+// residual after three terms is below 2^-12 of each 32-element block's max, bf16 operands
+// hold 8 significant bits): a K step's 4 weight blocks x 3 terms are 12 (block, term) pairs,
+// 4 per MFMA along K, so 3 MFMAs per step. K block j of MFMA m is the pair 4m + j = 3b + t:
+// its A operand is weight block b (native MXFP4 codes and scale byte, read per lane) and its
+// B operand term t of block b of the 16 pairs (with term t's scale byte). D then holds the
+// term-summed dot product of row x pair: no term columns to add afterwards, 16 pairs per
+// MFMA, and a wave keeps kGT x 2 accumulator tiles.
 // K advances 4 blocks per step:
 //   A: each row's 68 bytes of a step as 6 aligned 16-byte pieces, lane-contiguous (a wave
 //      load covers ~11 rows' contiguous bytes; 20-byte windows loaded per lane straight
@@ -183,9 +185,11 @@ constexpr int kASlots = kGT * 16 * kAPR;           // A pieces per wave and step
 constexpr int kAK = (kASlots + 63) / 64;           // A piece loads per lane and step
 constexpr int kARow = 104;  // LDS bytes per A row: 26 dwords, so 16 rows fall in 16 different banks
 constexpr int kBBuf = 2;                           // B stages in LDS
-static_assert(kBStep == 4 * kGW * 64 * 16, "four 16-byte pieces per thread per step");
+static_assert(kBStep == 4 * kGW * 64 * 16, "room for four 16-byte pieces per thread per step");
+constexpr int kBPieces = 3;  // 16-byte B pieces loaded per thread and step (terms 0-2)
+static_assert(kPairTile * 4 * 6 == kBPieces * kGW * 64, "the pieces of terms 0-2 fill the threads");
 static_assert(kPairTile * 4 == 2 * 64, "scale words: one per lane of waves 0-1");
-static_assert(kTerms == 4, "one term per MFMA K group");
+static_assert(kTerms == 4, "images of 4 terms (8 parts of 16 bytes per block); the GEMMs read terms 0-2");
 
 // LDS slot of 16-byte part q of (pair pr, block b) in a B stage: the 16 pairs that one read
 // instruction's lanes take (one part each) land in 16 different 16-byte bank groups.
@@ -256,16 +260,19 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     aslot[k] = (tt * 16 + rr) * kARow + apc[k] * 16;
   }
 
-  // B pieces of this thread: slot j*256 + tid = (pair j*8 + bpl, block bb, stored part bq)
-  const int bq = tid & 7, bb = (tid >> 3) & 3, bpl = tid >> 5;
-  const uint8_t* bsrc[4];
-  int bslot[4];
+  // B pieces of this thread: the step's 32 pairs x 4 blocks x the 6 16-byte parts of terms
+  // 0-2 (term 3 is not used) are 768 pieces, 3 per thread: piece j*256 + tid = (pair, block,
+  // part) in that order, so consecutive lanes read consecutive parts of a block
+  const uint8_t* bsrc[kBPieces];
+  int bslot[kBPieces], bblk[kBPieces];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    bslot[j] = b_slot(j * 8 + bpl, bb, bq);
-    const int p = p0 + min(j * 8 + bpl, np - 1);
+  for (int j = 0; j < kBPieces; ++j) {
+    const int q = j * 256 + tid, part = q % 6, blk = (q / 6) & 3, pr = q / 24;
+    bslot[j] = b_slot(pr, blk, part);
+    bblk[j] = blk;
+    const int p = p0 + min(pr, np - 1);
     const int r = a.pair_tok ? a.pair_tok[p] : p;
-    bsrc[j] = a.img + (size_t)r * nbK * kImgBytes + bq * 16;
+    bsrc[j] = a.img + (size_t)r * nbK * kImgBytes + part * 16;
   }
   const uint32_t* ssrc;  // scale word tid (waves 0-1): pair tid/4, block tid%4
   {
@@ -274,18 +281,20 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     ssrc = a.isc + (size_t)r * nbK;
   }
   struct BRegs {
-    i32x4 v[4];
+    i32x4 v[kBPieces];
     uint32_t sc;
   };
   auto load_b = [&](int st, BRegs& br) {
-    const size_t boff = (size_t)min(4 * st + bb, nbK - 1) * kImgBytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) br.v[j] = *(const __attribute__((address_space(1))) i32x4*)(bsrc[j] + boff);
+    for (int j = 0; j < kBPieces; ++j) {
+      const size_t boff = (size_t)min(4 * st + bblk[j], nbK - 1) * kImgBytes;
+      br.v[j] = *(const __attribute__((address_space(1))) i32x4*)(bsrc[j] + boff);
+    }
     br.sc = *(const __attribute__((address_space(1))) uint32_t*)(ssrc + min(4 * st + (tid & 3), nbK - 1));
   };
   auto store_b = [&](const BRegs& br, int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<i32x4*>(&bst[buf][bslot[j] * 16]) = br.v[j];
+    for (int j = 0; j < kBPieces; ++j) *reinterpret_cast<i32x4*>(&bst[buf][bslot[j] * 16]) = br.v[j];
     if (wave < 2) bsc[buf][tid] = br.sc;
   };
   auto load_a = [&](int st, i32x4 (&apv)[kAK]) {  // pieces past the row end read its last piece
@@ -307,14 +316,29 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
           d[1] = ((uint64_t)(uint32_t)apv[k][3] << 32) | (uint32_t)apv[k][2];
         }
   };
-  // B reads of lane (pair n = i of the group, K group g): parts g (term g/2, half g%2) and
-  // g + 4 (term 2 + g/2) of (pair, block); pairs of the two groups differ by 16 (same swizzle)
-  int brd[4][2];
+  // Per MFMA m of a step, lane (pair i of the group, K group g): the weight block of its A
+  // operand (K block g: pair 4m + g), the B parts it reads (B bytes 0-15 are K [16g, 16g+16),
+  // half g%2 of K block g/2; bytes 16-31 half g%2 of K block 2 + g/2; part 2t + half of
+  // (pair, block)), and its B scale byte (K block g: pair i, block b, term t at 16i + 4b + t).
+  // Pairs of the two groups differ by 16 (the same swizzle; scale bytes +256). Packed, as they
+  // stay live through the K loop: brdp[m] = the two B offsets (16 bits each); sap = per MFMA
+  // m, the scale byte offset (8 bits at 8m) and the A block (2 bits at 24 + 2m).
+  uint32_t brdp[3], sap = 0u;
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
+  for (int mm = 0; mm < 3; ++mm) {
+    const int pa = 4 * mm + g;
+    sap |= (uint32_t)(i * 16 + 4 * (pa / 3) + pa % 3) << (8 * mm);
+    sap |= (uint32_t)(pa / 3) << (24 + 2 * mm);
+    brdp[mm] = 0u;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) brd[k][h] = b_slot(i, k, g + 4 * h) * 16;
-  const int srd = i * 16 + g;  // scale byte of pair i, block 0, term g (block k: +4k; group: +256)
+    for (int h = 0; h < 2; ++h) {
+      const int pb = 4 * mm + 2 * h + (g >> 1);
+      brdp[mm] |= (uint32_t)(b_slot(i, pb / 3, 2 * (pb % 3) + (g & 1)) * 16) << (16 * h);
+    }
+  }
+  auto ablk = [&](int mm) { return (int)__builtin_amdgcn_ubfe(sap, 24u + 2u * (uint32_t)mm, 2u); };
+  auto srd = [&](int mm) { return (int)__builtin_amdgcn_ubfe(sap, 8u * (uint32_t)mm, 8u); };
+  auto brd = [&](int mm, int h) { return (int)__builtin_amdgcn_ubfe(brdp[mm], 16u * (uint32_t)h, 16u); };
 
   i32x4 apA[kAK], apB[kAK];
   BRegs bR;
@@ -342,16 +366,16 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     const uint8_t* bb_base = &bst[buf][0];
     const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
     const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
-    // Operands of block k: the A windows of this lane's rows (the 4 K groups of a row read the
-    // same window) and the 2 pair groups' B, read one block ahead of the MFMAs (reads of blocks
-    // past the row end stay inside the LDS stages; their MFMAs are skipped).
+    // Operands of MFMA mm: the A windows of this lane's rows (its block ablk[mm]) and the 2 pair
+    // groups' B, read one MFMA ahead (reads of blocks past the row end stay inside the LDS
+    // stages; such a lane's A codes are zero, so the block adds nothing).
     struct Ops {
       RawBlk r[kGT];
       i32x4 b[kPG][2];
       int sb[kPG];
     };
-    auto read_ops = [&](int k, Ops& o) {
-      const uint32_t wo = lead + 17u * (uint32_t)k;
+    auto read_ops = [&](int mm, Ops& o) {
+      const uint32_t wo = lead + 17u * (uint32_t)ablk(mm);
 #pragma unroll
       for (int tt = 0; tt < kGT; ++tt) {
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
@@ -361,22 +385,28 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 #pragma unroll
       for (int pg = 0; pg < kPG; ++pg) {
         const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
-        o.b[pg][0] = *reinterpret_cast<const i32x4*>(bp + brd[k][0]);
-        o.b[pg][1] = *reinterpret_cast<const i32x4*>(bp + brd[k][1]);
-        o.sb[pg] = (int)sc_base[srd + pg * 256 + 4 * k];
+        o.b[pg][0] = *reinterpret_cast<const i32x4*>(bp + brd(mm, 0));
+        o.b[pg][1] = *reinterpret_cast<const i32x4*>(bp + brd(mm, 1));
+        o.sb[pg] = (int)sc_base[srd(mm) + pg * 256];
       }
     };
-    auto run_ops = [&](int k, const Ops& o) {
-      const uint32_t wo = lead + 17u * (uint32_t)k;
-      const uint32_t t8 = 8u * ((wo & 3u) + 1u);
+    auto run_ops = [&](int mm, const Ops& o) {
+      const uint32_t wo = lead + 17u * (uint32_t)ablk(mm);
+      const uint32_t t = (wo & 3u) + 1u;  // the codes start t bytes into the window (1..4)
+      const bool valid = 4 * st + ablk(mm) < nbK;
       AOp ao[kGT];
       int sa[kGT];
 #pragma unroll
       for (int tt = 0; tt < kGT; ++tt) {
+        // byte alignment by v_alignbyte (a shift of 4 bytes selects the upper dword): the same
+        // as shifting the dword pair right by t bytes, which the compiler would otherwise do
+        // through a stack copy of the window
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          ao[tt].q[q] = (uint32_t)((((uint64_t)o.r[tt].d[q + 1] << 32) | o.r[tt].d[q]) >> t8);
-        sa[tt] = (int)((o.r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu);
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t v = t == 4u ? o.r[tt].d[q + 1] : __builtin_amdgcn_alignbyte(o.r[tt].d[q + 1], o.r[tt].d[q], t);
+          ao[tt].q[q] = valid ? v : 0u;
+        }
+        sa[tt] = valid ? (int)((o.r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu) : 127;
       }
 #pragma unroll
       for (int pg = 0; pg < kPG; ++pg) {
@@ -392,12 +422,10 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     Ops o0, o1;
     read_ops(0, o0);
     read_ops(1, o1);
-    if (4 * st + 0 < nbK) run_ops(0, o0);  // uniform: blocks past the row end are skipped
+    run_ops(0, o0);
     read_ops(2, o0);
-    if (4 * st + 1 < nbK) run_ops(1, o1);
-    read_ops(3, o1);
-    if (4 * st + 2 < nbK) run_ops(2, o0);
-    if (4 * st + 3 < nbK) run_ops(3, o1);
+    run_ops(1, o1);
+    run_ops(2, o0);
   };
   int st = 0;
   for (; st + 1 < S; st += 2) {
