@@ -183,7 +183,11 @@ constexpr int kBStep = kPairTile * 4 * kImgBytes;  // B bytes per K step
 constexpr int kAPR = 6;                            // A pieces per row and step: 68 bytes at any offset
 constexpr int kASlots = kGT * 16 * kAPR;           // A pieces per wave and step
 constexpr int kAK = (kASlots + 63) / 64;           // A piece loads per lane and step
-constexpr int kARow = 104;  // LDS bytes per A row: 26 dwords, so 16 rows fall in 16 different banks
+#ifndef MR_GROUPED_AROW
+#define MR_GROUPED_AROW 104
+#endif
+constexpr int kARow = MR_GROUPED_AROW;  // LDS bytes per A row: 26 dwords, so 16 rows fall in 16 different banks
+static_assert(kARow % 4 == 0 && kARow >= 6 * 16, "an A row holds a step's 6 pieces, dword-aligned");
 constexpr int kBBuf = 2;                           // B stages in LDS
 static_assert(kBStep == 4 * kGW * 64 * 16, "room for four 16-byte pieces per thread per step");
 constexpr int kBPieces = 3;  // 16-byte B pieces loaded per thread and step (terms 0-2)
@@ -310,10 +314,15 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 #pragma unroll
     for (int k = 0; k < kAK; ++k)
       if (k * 64 + 64 <= kASlots || k * 64 + lane < kASlots)
-        {  // 8-byte aligned: rows are kARow bytes apart
-          uint64_t* d = reinterpret_cast<uint64_t*>(&ast[wave][aslot[k]]);
-          d[0] = ((uint64_t)(uint32_t)apv[k][1] << 32) | (uint32_t)apv[k][0];
-          d[1] = ((uint64_t)(uint32_t)apv[k][3] << 32) | (uint32_t)apv[k][2];
+        {
+          if constexpr (kARow % 8 == 0) {  // 8-byte aligned: rows are kARow bytes apart
+            uint64_t* d = reinterpret_cast<uint64_t*>(&ast[wave][aslot[k]]);
+            d[0] = ((uint64_t)(uint32_t)apv[k][1] << 32) | (uint32_t)apv[k][0];
+            d[1] = ((uint64_t)(uint32_t)apv[k][3] << 32) | (uint32_t)apv[k][2];
+          } else {
+            uint32_t* d = reinterpret_cast<uint32_t*>(&ast[wave][aslot[k]]);
+            d[0] = (uint32_t)apv[k][0], d[1] = (uint32_t)apv[k][1], d[2] = (uint32_t)apv[k][2], d[3] = (uint32_t)apv[k][3];
+          }
         }
   };
   // Per MFMA m of a step, lane (pair i of the group, K group g): the weight block of its A
