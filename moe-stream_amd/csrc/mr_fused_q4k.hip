@@ -53,6 +53,11 @@ constexpr int kQ4RingG = 4;       // gate/up units loaded ahead (two rounds: H/5
 constexpr int kQ4RingD = 6;       // down units loaded ahead (two rounds: ceil(ktot/4) * I/256 <= 12)
 constexpr int kQ4MaxH = 4096, kQ4MaxI = 2048, kQ4MaxKI = 12288, kQ4MaxSlots = 17;
 constexpr int kQ4MaxUnitsD = 2 * kQ4RingD;          // down units of one wave
+#ifndef MR_Q4_PRESPLIT
+#define MR_Q4_PRESPLIT 6  // all: C3 15.62 -> 15.31 us, C4 16.73 -> 16.38 us (2 and 4 gain less)
+#endif
+constexpr int kQ4PreSplit = MR_Q4_PRESPLIT;         // down units whose B operands are split before the wait
+static_assert(kQ4PreSplit >= 0 && kQ4PreSplit <= kQ4RingD, "at most every ring unit");
 
 // LDS carve-up (bytes): activation image [groups][2 terms][16 int8] (gate/up: x, H/16 groups;
 // down: h of every slot, ktot * I/16 groups), group scales [groups] (s0/256, sum), a zero
@@ -573,13 +578,21 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       // every unit's sub-block scales are decoded while the gate/up results are awaited (the
       // weights land long before the count completes; the scales take the header's registers)
+      // The first kQ4PreSplit units (all of them by default) also get their nibbles split into
+      // the int8 B operands here, so after the wait only the LDS operands, the MFMAs and the
+      // epilogue remain per unit.
       [[maybe_unused]] UnitScales US[STREAM ? 1 : kQ4RingD];
+      [[maybe_unused]] UnitPrep PS[STREAM ? 1 : kQ4PreSplit];
       if constexpr (!STREAM) {
 #pragma unroll
         for (int r = 0; r < kQ4RingD; ++r) {
           US[r] = unit_scales(R.hd[r], ul);
           // materialised here: the compiler would otherwise sink the decode to its use
           asm volatile("" : "+v"(US[r].dsc[0]), "+v"(US[r].dsc[1]), "+v"(US[r].dm[0]), "+v"(US[r].dm[1]));
+          if (r < kQ4PreSplit) {
+            PS[r] = unit_prep(US[r], R.w0[r], R.w1[r]);
+            asm volatile("" : "+v"(PS[r].b[0][0]), "+v"(PS[r].b[0][1]), "+v"(PS[r].b[1][0]), "+v"(PS[r].b[1][1]));
+          }
         }
       }
       TRACE(2);
@@ -617,7 +630,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
             const UnitOps cur = op;
             if (r + 1 < kQ4RingD)
               op = unit_ops(ul, (uint32_t)(sj[(r + 1) / DN] * nGI + ((r + 1) % DN) * 16), smem);
-            acc += unit_dot(unit_prep(US[r], R.w0[r], R.w1[r]), cur);
+            acc += unit_dot(r < kQ4PreSplit ? PS[r < kQ4PreSplit ? r : 0] : unit_prep(US[r], R.w0[r], R.w1[r]), cur);
             if (c == DN - 1) {  // the slot's last super-block: lanes 0-15 store its rows (repeated
                                 // slots and the other lanes store to this wave's spare row)
               acc = row_total(acc);
