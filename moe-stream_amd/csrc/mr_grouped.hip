@@ -7,15 +7,15 @@
 //   k_group       (token, slot) pairs grouped by expert; per-expert pair offsets and
 //                 32-pair tile offsets; pair index of every (token, slot).
 //   k_split_rows  x rows -> e4m3 B images (4 terms per 32-element block).
-//   k_grouped_gemm<true>   gate and up for one (expert, 96-row tile, 32-pair tile):
+//   k_grouped_gemm<true>   gate and up for one (expert, 128-row tile, 32-pair tile):
 //                 A = native MXFP4 weight rows, B = the pairs' x images; epilogue
 //                 bias + activation x routing weight, split into the h images
 //                 [pair][I/32] (the split of k_split_rows).
-//   k_grouped_gemm<false>  down for one (expert, 192-row tile, 32-pair tile) on the
+//   k_grouped_gemm<false>  down for one (expert, 256-row tile, 32-pair tile) on the
 //                 h images -> o [pair][H].
 //   k_combine     y[t] = sum over t's pairs in ascending expert order of
 //                 (o + w*b_down) (the order of layer.rs:1092-1106).
-// Every weight byte of an expert is read by the ceil(n_e/16) pair tiles of its
+// Every weight byte of an expert is read by the ceil(n_e/32) pair tiles of its
 // row tiles; work items are laid out so those repeats, and the repeats of the
 // pairs' activation images over row tiles, hit the same XCD's L2.
 #include "mr_device.h"
@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 namespace mr {
 
@@ -155,16 +156,17 @@ struct GroupedArgs {
 };
 
 // Grouped GEMM work item: (expert e, row tile, 32-pair tile); 4 waves. A wave owns kGT
-// 16-row A tiles of one matrix (gate/up: waves 0-1 gate, 2-3 up, the same 96 rows; down:
-// 4 x 48 = 192 rows) and the tile's 32 pairs as 2 groups of 16.
+// 16-row A tiles of one matrix (gate/up: waves 0-1 gate, 2-3 up, the same 128 rows; down:
+// 4 x 64 = 256 rows) and the tile's 32 pairs as 2 groups of 16.
 // The MFMAs take the first kGemmTerms = 3 e4m3 terms of the pairs' activation split (the
 // residual after three terms is below 2^-12 of each 32-element block's max, bf16 operands
-// hold 8 significant bits): a K step's 4 weight blocks x 3 terms are 12 (block, term) pairs,
-// 4 per MFMA along K, so 3 MFMAs per step. K block j of MFMA m is the pair 4m + j = 3b + t:
-// its A operand is weight block b (native MXFP4 codes and scale byte, read per lane) and its
-// B operand term t of block b of the 16 pairs (with term t's scale byte). D then holds the
-// term-summed dot product of row x pair: no term columns to add afterwards, 16 pairs per
-// MFMA, and a wave keeps kGT x 2 accumulator tiles.
+// hold 8 significant bits). A K step holds 4 weight blocks; MFMA m of the step takes term m of
+// all four: K block j of MFMA m is weight block j (its A operand: native MXFP4 codes and the
+// block's scale byte, read per lane) against term m of block j of the 16 pairs (with that
+// term's scale byte). A lane's A operand is then the same in the step's 3 MFMAs, so each A
+// window is read from LDS and aligned once per step, and D accumulates the term-summed dot
+// product of row x pair: no term columns to add afterwards, 16 pairs per MFMA, and a wave
+// keeps kGT x 2 accumulator tiles.
 // K advances 4 blocks per step:
 //   A: each row's 68 bytes of a step as 6 aligned 16-byte pieces, lane-contiguous (a wave
 //      load covers ~11 rows' contiguous bytes; 20-byte windows loaded per lane straight
@@ -177,12 +179,18 @@ struct GroupedArgs {
 //      prefetch.) 16-byte part q of (pair pr, block b) sits in slot b_slot(pr, b, q),
 //      so the 16 lanes of a read (16 pairs, one part) hit 16 different bank groups.
 constexpr int kGW = 4;               // waves per work item
-constexpr int kGT = 3;               // 16-row A tiles per wave
+#ifndef MR_GROUPED_GT_GU
+#define MR_GROUPED_GT_GU 4
+#endif
+#ifndef MR_GROUPED_GT_DN
+#define MR_GROUPED_GT_DN 4
+#endif
+// 16-row A tiles per wave (gate/up, down) and the rows of a matrix per work item
+template <bool GATEUP> constexpr int kGTof = GATEUP ? MR_GROUPED_GT_GU : MR_GROUPED_GT_DN;
+template <bool GATEUP> constexpr int kRowsOf = (GATEUP ? kGW / 2 : kGW) * kGTof<GATEUP> * 16;
 constexpr int kPG = kPairTile / 16;  // 16-pair MFMA column groups
 constexpr int kBStep = kPairTile * 4 * kImgBytes;  // B bytes per K step
 constexpr int kAPR = 6;                            // A pieces per row and step: 68 bytes at any offset
-constexpr int kASlots = kGT * 16 * kAPR;           // A pieces per wave and step
-constexpr int kAK = (kASlots + 63) / 64;           // A piece loads per lane and step
 #ifndef MR_GROUPED_AROW
 #define MR_GROUPED_AROW 104
 #endif
@@ -203,13 +211,16 @@ template <bool GATEUP>
 __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   __shared__ __align__(16) uint8_t bst[kBBuf][kBStep];
   __shared__ __align__(16) uint32_t bsc[kBBuf][kPairTile * 4];
+  constexpr int kGT = kGTof<GATEUP>;               // 16-row A tiles per wave
+  constexpr int kASlots = kGT * 16 * kAPR;         // A pieces per wave and step
+  constexpr int kAK = (kASlots + 63) / 64;         // A piece loads per lane and step
   __shared__ __align__(16) uint8_t ast[kGW][kGT * 16 * kARow];
   __shared__ float bias_s[GATEUP ? 2 * (kGW / 2) * kGT * 16 + kPairTile : 1];  // GATEUP: the tile's gate,
                                                                                // up biases, pair weights
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: wave-level branches stay scalar
   const int i = lane & 15, g = lane >> 4;
-  constexpr int kRows = GATEUP ? (kGW / 2) * kGT * 16 : kGW * kGT * 16;  // rows of a matrix per item
+  constexpr int kRows = kRowsOf<GATEUP>;  // rows of a matrix per item
   // Work items are ordered (expert, row tile, pair tile of the expert), and each XCD
   // (workgroups are dispatched round-robin over kXcds) takes one contiguous range of them:
   // the items that share an expert's row tile (A) or its pairs' images (B) run on the same
@@ -237,13 +248,17 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   const uint64_t rb = (uint64_t)nbK * 17;
   const int m = GATEUP ? (wave >> 1) : 0;
   const int wrow0 = rt * kRows + (GATEUP ? (wave & 1) : wave) * (kGT * 16);
-  if (GATEUP && tid < 2 * kRows) {  // read by the epilogue (after the K loop's barriers)
-    const int mat = tid >= kRows, orow = rt * kRows + tid - mat * kRows;
-    const float* bsrc = mat ? a.b1 : a.b0;
-    bias_s[tid] = (bsrc && orow < a.M) ? bsrc[(size_t)e * a.M + orow] : 0.f;
+  if (GATEUP) {  // read by the epilogue (after the K loop's barriers)
+    for (int q = tid; q < 2 * kRows + kPairTile; q += kGW * 64) {
+      if (q < 2 * kRows) {
+        const int mat = q >= kRows, orow = rt * kRows + q - mat * kRows;
+        const float* bsrc = mat ? a.b1 : a.b0;
+        bias_s[q] = (bsrc && orow < a.M) ? bsrc[(size_t)e * a.M + orow] : 0.f;
+      } else {
+        bias_s[q] = a.pair_w[p0 + min(q - 2 * kRows, np - 1)];
+      }
+    }
   }
-  if (GATEUP && tid >= 2 * kRows && tid < 2 * kRows + kPairTile)
-    bias_s[tid] = a.pair_w[p0 + min(tid - 2 * kRows, np - 1)];
   const uint8_t* W = expert_at(m ? a.w1 : a.w0, e);
   bool tin[kGT];  // tile inside the matrix (wave-uniform)
 #pragma unroll
@@ -325,29 +340,18 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
           }
         }
   };
-  // Per MFMA m of a step, lane (pair i of the group, K group g): the weight block of its A
-  // operand (K block g: pair 4m + g), the B parts it reads (B bytes 0-15 are K [16g, 16g+16),
-  // half g%2 of K block g/2; bytes 16-31 half g%2 of K block 2 + g/2; part 2t + half of
-  // (pair, block)), and its B scale byte (K block g: pair i, block b, term t at 16i + 4b + t).
-  // Pairs of the two groups differ by 16 (the same swizzle; scale bytes +256). Packed, as they
-  // stay live through the K loop: brdp[m] = the two B offsets (16 bits each); sap = per MFMA
-  // m, the scale byte offset (8 bits at 8m) and the A block (2 bits at 24 + 2m).
-  uint32_t brdp[3], sap = 0u;
+  // MFMA m of a step takes term m of the activation split for all 4 blocks of the step. Lane
+  // (pair i of the group, K group g): its A operand is weight block g of the step in all three
+  // MFMAs; its B bytes 0-15 are K [16g, 16g+16), half g%2 of K block g/2, and bytes 16-31 half
+  // g%2 of K block 2 + g/2, i.e. part 2m + g%2 of (pair i, block g/2) and of (pair i, block
+  // 2 + g/2), which b_slot places 16 slots (256 bytes) further; its B scale byte is (pair i,
+  // block g, term m) at 16i + 4g + m. Pairs of the two groups differ by 16 (the same swizzle;
+  // scale bytes +256). brdp holds the slot of MFMA m's first part in bits 10m .. 10m + 9.
+  uint32_t brdp = 0u;
 #pragma unroll
-  for (int mm = 0; mm < 3; ++mm) {
-    const int pa = 4 * mm + g;
-    sap |= (uint32_t)(i * 16 + 4 * (pa / 3) + pa % 3) << (8 * mm);
-    sap |= (uint32_t)(pa / 3) << (24 + 2 * mm);
-    brdp[mm] = 0u;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int pb = 4 * mm + 2 * h + (g >> 1);
-      brdp[mm] |= (uint32_t)(b_slot(i, pb / 3, 2 * (pb % 3) + (g & 1)) * 16) << (16 * h);
-    }
-  }
-  auto ablk = [&](int mm) { return (int)__builtin_amdgcn_ubfe(sap, 24u + 2u * (uint32_t)mm, 2u); };
-  auto srd = [&](int mm) { return (int)__builtin_amdgcn_ubfe(sap, 8u * (uint32_t)mm, 8u); };
-  auto brd = [&](int mm, int h) { return (int)__builtin_amdgcn_ubfe(brdp[mm], 16u * (uint32_t)h, 16u); };
+  for (int mm = 0; mm < 3; ++mm) brdp |= (uint32_t)b_slot(i, g >> 1, 2 * mm + (g & 1)) << (10 * mm);
+  const int sc_lane = i * 16 + 4 * g;
+  auto brd = [&](int mm) { return (int)(__builtin_amdgcn_ubfe(brdp, 10u * (uint32_t)mm, 10u) * 16u); };
 
   i32x4 apA[kAK], apB[kAK];
   BRegs bR;
@@ -365,7 +369,10 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   // register set (one step ahead: the images are L2 hits), B in LDS buffer st % 2. Every step
   // issues the same loads, B first (past the last step: the last step's data again), so the
   // compiler's waits before the LDS writes count exactly the loads issued after them.
-  auto step = [&](int st, i32x4 (&cur)[kAK]) {
+  // `part` (a std::bool_constant): the step may hold blocks past the row end. Only such steps
+  // test every A window for it; full steps compile without those selects.
+  auto step = [&](int st, i32x4 (&cur)[kAK], auto part) {
+    constexpr bool kPart = decltype(part)::value;
     const int buf = st % kBBuf;
     store_a(cur);      // this wave's A slice (its reads of step st-1 are done: LDS ops stay in order)
     store_b(bR, buf);  // buffer st % 2 was last read in step st-2, before the previous barrier
@@ -375,48 +382,50 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     const uint8_t* bb_base = &bst[buf][0];
     const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
     const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
-    // Operands of MFMA mm: the A windows of this lane's rows (its block ablk[mm]) and the 2 pair
-    // groups' B, read one MFMA ahead (reads of blocks past the row end stay inside the LDS
-    // stages; such a lane's A codes are zero, so the block adds nothing).
-    struct Ops {
-      RawBlk r[kGT];
+    // B operands of MFMA mm for the 2 pair groups, read one MFMA ahead; the A operands (this
+    // lane's block g of each tile's row i) once per step for all three MFMAs. A block past the
+    // row end (read inside the LDS stage) gets zero codes, so it adds nothing.
+    struct BOps {
       i32x4 b[kPG][2];
       int sb[kPG];
     };
-    auto read_ops = [&](int mm, Ops& o) {
-      const uint32_t wo = lead + 17u * (uint32_t)ablk(mm);
-#pragma unroll
-      for (int tt = 0; tt < kGT; ++tt) {
-        const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
-        o.r[tt].d[0] = wp[0], o.r[tt].d[1] = wp[1], o.r[tt].d[2] = wp[2], o.r[tt].d[3] = wp[3],
-        o.r[tt].d[4] = wp[4];
-      }
+    auto read_b = [&](int mm, BOps& o) {
+      const int off = brd(mm);
 #pragma unroll
       for (int pg = 0; pg < kPG; ++pg) {
-        const uint8_t* bp = bb_base + pg * 16 * 32 * 16;  // pairs 16 further: same swizzle
-        o.b[pg][0] = *reinterpret_cast<const i32x4*>(bp + brd(mm, 0));
-        o.b[pg][1] = *reinterpret_cast<const i32x4*>(bp + brd(mm, 1));
-        o.sb[pg] = (int)sc_base[srd(mm) + pg * 256];
+        const uint8_t* bp = bb_base + pg * 16 * 32 * 16 + off;  // pairs 16 further: same swizzle
+        o.b[pg][0] = *reinterpret_cast<const i32x4*>(bp);
+        o.b[pg][1] = *reinterpret_cast<const i32x4*>(bp + 256);
+        o.sb[pg] = (int)sc_base[sc_lane + mm + pg * 256];
       }
     };
-    auto run_ops = [&](int mm, const Ops& o) {
-      const uint32_t wo = lead + 17u * (uint32_t)ablk(mm);
-      const uint32_t t = (wo & 3u) + 1u;  // the codes start t bytes into the window (1..4)
-      const bool valid = 4 * st + ablk(mm) < nbK;
-      AOp ao[kGT];
-      int sa[kGT];
+    const uint32_t wo = lead + 17u * (uint32_t)g;  // block g's scale byte in the row's LDS slice
+    RawBlk r[kGT];
 #pragma unroll
-      for (int tt = 0; tt < kGT; ++tt) {
-        // byte alignment by v_alignbyte (a shift of 4 bytes selects the upper dword): the same
-        // as shifting the dword pair right by t bytes, which the compiler would otherwise do
-        // through a stack copy of the window
+    for (int tt = 0; tt < kGT; ++tt) {
+      const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
+      r[tt].d[0] = wp[0], r[tt].d[1] = wp[1], r[tt].d[2] = wp[2], r[tt].d[3] = wp[3], r[tt].d[4] = wp[4];
+    }
+    BOps o0, o1;
+    read_b(0, o0);
+    read_b(1, o1);
+    const uint32_t t = (wo & 3u) + 1u;  // the codes start t bytes into the window (1..4)
+    const bool valid = !kPart || 4 * st + g < nbK;
+    AOp ao[kGT];
+    int sa[kGT];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t v = t == 4u ? o.r[tt].d[q + 1] : __builtin_amdgcn_alignbyte(o.r[tt].d[q + 1], o.r[tt].d[q], t);
-          ao[tt].q[q] = valid ? v : 0u;
-        }
-        sa[tt] = valid ? (int)((o.r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu) : 127;
+    for (int tt = 0; tt < kGT; ++tt) {
+      // byte alignment by v_alignbyte (a shift of 4 bytes selects the upper dword): the same
+      // as shifting the dword pair right by t bytes, which the compiler would otherwise do
+      // through a stack copy of the window
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t v = t == 4u ? r[tt].d[q + 1] : __builtin_amdgcn_alignbyte(r[tt].d[q + 1], r[tt].d[q], t);
+        ao[tt].q[q] = valid ? v : 0u;
       }
+      sa[tt] = valid ? (int)((r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu) : 127;
+    }
+    auto run_b = [&](const BOps& o) {
 #pragma unroll
       for (int pg = 0; pg < kPG; ++pg) {
         if (pg < npg) {
@@ -428,20 +437,23 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
         }
       }
     };
-    Ops o0, o1;
-    read_ops(0, o0);
-    read_ops(1, o1);
-    run_ops(0, o0);
-    read_ops(2, o0);
-    run_ops(1, o1);
-    run_ops(2, o0);
+    run_b(o0);
+    read_b(2, o0);
+    run_b(o1);
+    run_b(o0);
   };
+  // Steps 0 .. nbK/4 - 1 hold only blocks inside the row; the one or two steps after the loop
+  // (the last one possibly partial) run the checked variant.
+  const int s_full = nbK >> 2;
   int st = 0;
-  for (; st + 1 < S; st += 2) {
-    step(st, apA);
-    step(st + 1, apB);
+  for (; st + 1 < s_full; st += 2) {
+    step(st, apA, std::false_type{});
+    step(st + 1, apB, std::false_type{});
   }
-  if (st < S) step(st, apA);
+  if (st < S) {
+    step(st, apA, std::true_type{});
+    if (st + 1 < S) step(st + 1, apB, std::true_type{});
+  }
 
   // Epilogue: acc[tt][pg][r] of lane (i, g) is row wrow0 + 16 tt + 4g + r x pair 16 pg + i.
   // The wave's block goes through LDS as [pair][row] so that each pair's rows are stored
@@ -668,7 +680,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   {
     ProfScope ps(K, "grouped_gateup");
-    constexpr int rows = (kGW / 2) * kGT * 16;
+    constexpr int rows = kRowsOf<true>;
     hipLaunchKernelGGL(k_grouped_gemm<true>, dim3(grouped_grid((uint64_t)((I + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
                        K.s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -680,7 +692,7 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
   d.M = H, d.K = I, d.E = E;
   {
     ProfScope ps(K, "grouped_down");
-    constexpr int rows = kGW * kGT * 16;
+    constexpr int rows = kRowsOf<false>;
     hipLaunchKernelGGL(k_grouped_gemm<false>, dim3(grouped_grid((uint64_t)((H + rows - 1) / rows) * max_tiles)), dim3(kGW * 64), 0,
                        K.s, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
