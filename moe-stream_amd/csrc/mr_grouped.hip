@@ -6,7 +6,7 @@
 // (layer.rs:2148-2183; CPU: mxfp4_matmul per expert, layer.rs:1449-1514). Here:
 //   k_group       (token, slot) pairs grouped by expert; per-expert pair offsets and
 //                 32-pair tile offsets; pair index of every (token, slot).
-//   k_split_rows  x rows -> e4m3 B images (4 terms per 32-element block).
+//   k_split_rows  x rows -> e4m3 B images (terms 0-2 of the split of each 32-element block).
 //   k_grouped_gemm<true>   gate and up for one (expert, 128-row tile, 32-pair tile):
 //                 A = native MXFP4 weight rows, B = the pairs' x images; epilogue
 //                 bias + activation x routing weight, split into the h images
@@ -28,6 +28,10 @@
 #include <type_traits>
 
 namespace mr {
+
+// Terms of the activation split that the grouped GEMMs read, and all that their splits
+// compute and write (the images keep the 4-term layout; term 3 is left unwritten).
+constexpr int kGemmTerms = 3;
 
 constexpr int kPairTile = 32;   // pairs (tokens) per work item = 8 MFMA column groups x 4
 constexpr int kXcds = 8;        // MI355X accelerator complex dies (one L2 each)
@@ -124,12 +128,12 @@ __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ sr
     const f32x2 lo = *reinterpret_cast<const f32x2*>(p);       // elements 2m, 2m+1
     const f32x2 hi = *reinterpret_cast<const f32x2*>(p + 16);  // elements 2m+16, 2m+17
     uint32_t codes[kTerms], scales;
-    split_block8(lo.x, hi.x, lo.y, hi.y, codes, scales);
+    split_block8<kGemmTerms>(lo.x, hi.x, lo.y, hi.y, codes, scales);
     if (in) {
       const size_t bb = (size_t)r * nb + b;
       uint32_t* dst = reinterpret_cast<uint32_t*>(img + bb * kImgBytes);
 #pragma unroll
-      for (int t = 0; t < kTerms; ++t) dst[t * 8 + m] = codes[t];
+      for (int t = 0; t < kGemmTerms; ++t) dst[t * 8 + m] = codes[t];
       if (m == 0) sc[bb] = scales;
     }
   }
@@ -456,60 +460,65 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   }
 
   // Epilogue: acc[tt][pg][r] of lane (i, g) is row wrow0 + 16 tt + 4g + r x pair 16 pg + i.
-  // The wave's block goes through LDS as [pair][row] so that each pair's rows are stored
-  // contiguously (and the up waves find the gate values of their rows there).
+  if constexpr (!GATEUP) {  // down: the lane's 4 consecutive rows of a pair as one 16-byte store
+#pragma unroll
+    for (int tt = 0; tt < kGT; ++tt)
+#pragma unroll
+      for (int pg = 0; pg < kPG; ++pg) {
+        const int pl = pg * 16 + i, row = wrow0 + 16 * tt + 4 * g;  // M % 32 == 0: row < M -> row + 3 < M
+        if (pl < np && row < a.M) *reinterpret_cast<f32x4*>(a.out + (size_t)(p0 + pl) * a.M + row) = acc[tt][pg];
+      }
+    return;
+  }
+  // Gate/up: the wave's block goes through LDS as [pair][row] so that each pair's rows are stored
+  // contiguously (and the up waves find the gate values of their rows there). Row rr of pair
+  // pl sits at rr ^ 4 (pl % 16) within the pair's kWR words: the 16 pairs of one write (a
+  // row stride of kWR = 64 words would put them all in one bank) spread over 16 bank groups.
   __syncthreads();  // the K loop's LDS is no longer read
   constexpr int kWR = kGT * 16;                                  // rows of a wave
+  constexpr int kSwz = (kWR >= 64 && (kWR & (kWR - 1)) == 0) ? 15 : 0;  // XOR stays inside kWR
+  auto at_pr = [&](int pl, int rr) { return pl * kWR + (rr ^ ((pl & kSwz) << 2)); };
   float* blk = reinterpret_cast<float*>(&bst[0][0]) + wave * kPairTile * kWR;  // [pair][row]
 #pragma unroll
   for (int tt = 0; tt < kGT; ++tt)
 #pragma unroll
     for (int pg = 0; pg < kPG; ++pg)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) blk[(pg * 16 + i) * kWR + tt * 16 + 4 * g + r] = acc[tt][pg][r];
+      for (int r = 0; r < 4; ++r) blk[at_pr(pg * 16 + i, tt * 16 + 4 * g + r)] = acc[tt][pg][r];
   __syncthreads();
-  if (GATEUP) {
-    // h = act(gate, up) x routing weight over the gate values, by all four waves: the blocks
-    // of gate waves 0 and 1 then hold h of tile rows 0-47 and 48-95 ([pair][row] each)
-    float* ldsf = reinterpret_cast<float*>(&bst[0][0]);
-    for (int q = tid; q < np * kRows; q += kGW * 64) {
-      const int pl = q / kRows, r = q - pl * kRows;
-      if (rt * kRows + r >= a.M) continue;
-      const int half = r >= kWR ? 1 : 0, at = (half * kPairTile + pl) * kWR + r - half * kWR;
-      float gv = ldsf[at], uv = ldsf[2 * kPairTile * kWR + at];
-      if (a.b0) gv = gv + bias_s[r];
-      if (a.b1) uv = uv + bias_s[kRows + r];
-      const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-      ldsf[at] = h * bias_s[2 * kRows + pl];
-    }
-    __syncthreads();
-    // each (pair, 32-row block) of the tile split into the down input image (the split of
-    // k_split_rows, 8 lanes per block: lane m8 takes elements 2m8, 2m8+16, 2m8+1, 2m8+17)
-    const float* hb = reinterpret_cast<const float*>(&bst[0][0]);
-    const int tr0 = rt * kRows, nbM = a.M >> 5;
-    const int nblk = min(kRows, a.M - tr0) >> 5;  // blocks of this tile (M % 32 == 0)
-    const int m8 = tid & 7;
-    auto hval = [&](int pl, int r) {  // h of tile row r (< 96), pair pl
-      const int half = r >= kWR ? 1 : 0;
-      return hb[(half * kPairTile + pl) * kWR + r - half * kWR];
-    };
-    for (int u = tid >> 3; u < np * nblk; u += kGW * 8) {  // a whole 8-lane group per unit
-      const int pl = u / nblk, b = u - pl * nblk, r0 = 32 * b + 2 * m8;
-      uint32_t codes[kTerms], scales;
-      split_block8(hval(pl, r0), hval(pl, r0 + 16), hval(pl, r0 + 1), hval(pl, r0 + 17), codes, scales);
-      const size_t bi = (size_t)(p0 + pl) * nbM + (tr0 >> 5) + b;
-      uint32_t* dst = reinterpret_cast<uint32_t*>(a.himg + bi * kImgBytes);
-#pragma unroll
-      for (int t = 0; t < kTerms; ++t) dst[t * 8 + m8] = codes[t];
-      if (m8 == 0) a.hsc[bi] = scales;
-    }
-    return;
+  // h = act(gate, up) x routing weight over the gate values, by all four waves: the blocks
+  // of gate waves 0 and 1 then hold h of the tile rows 0 .. kWR-1 and kWR .. 2kWR-1 ([pair][row] each)
+  float* ldsf = reinterpret_cast<float*>(&bst[0][0]);
+  for (int q = tid; q < np * kRows; q += kGW * 64) {
+    const int pl = q / kRows, r = q - pl * kRows;
+    if (rt * kRows + r >= a.M) continue;
+    const int half = r >= kWR ? 1 : 0, at = half * kPairTile * kWR + at_pr(pl, r - half * kWR);
+    float gv = ldsf[at], uv = ldsf[2 * kPairTile * kWR + at];
+    if (a.b0) gv = gv + bias_s[r];
+    if (a.b1) uv = uv + bias_s[kRows + r];
+    const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
+    ldsf[at] = h * bias_s[2 * kRows + pl];
   }
-  for (int q = lane; q < np * kWR; q += 64) {
-    const int pl = q / kWR, rr = q - pl * kWR;
-    const int orow = wrow0 + rr;
-    if (orow >= a.M) continue;
-    a.out[(size_t)(p0 + pl) * a.M + orow] = blk[pl * kWR + rr];
+  __syncthreads();
+  // each (pair, 32-row block) of the tile split into the down input image (the split of
+  // k_split_rows, 8 lanes per block: lane m8 takes elements 2m8, 2m8+16, 2m8+1, 2m8+17)
+  const float* hb = reinterpret_cast<const float*>(&bst[0][0]);
+  const int tr0 = rt * kRows, nbM = a.M >> 5;
+  const int nblk = min(kRows, a.M - tr0) >> 5;  // blocks of this tile (M % 32 == 0)
+  const int m8 = tid & 7;
+  auto hval = [&](int pl, int r) {  // h of tile row r (< kRows), pair pl
+    const int half = r >= kWR ? 1 : 0;
+    return hb[half * kPairTile * kWR + at_pr(pl, r - half * kWR)];
+  };
+  for (int u = tid >> 3; u < np * nblk; u += kGW * 8) {  // a whole 8-lane group per unit
+    const int pl = u / nblk, b = u - pl * nblk, r0 = 32 * b + 2 * m8;
+    uint32_t codes[kTerms], scales;
+    split_block8<kGemmTerms>(hval(pl, r0), hval(pl, r0 + 16), hval(pl, r0 + 1), hval(pl, r0 + 17), codes, scales);
+    const size_t bi = (size_t)(p0 + pl) * nbM + (tr0 >> 5) + b;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(a.himg + bi * kImgBytes);
+#pragma unroll
+    for (int t = 0; t < kGemmTerms; ++t) dst[t * 8 + m8] = codes[t];
+    if (m8 == 0) a.hsc[bi] = scales;
   }
 }
 

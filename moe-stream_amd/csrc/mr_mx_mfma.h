@@ -35,13 +35,18 @@ constexpr int kImgBytes = kTerms * 32;  // B image bytes per 32-element block
 // Term t: scale 2^(floor(log2 max|r_t|) - 7) so max|r_t|/scale is in [128, 256);
 // codes by v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even); the residual
 // after kTerms terms is below 2^-16 of the block max. codes[t] is the code
-// dword of term t; the kTerms scale bytes are packed into `scales`.
+// dword of term t; the kTerms scale bytes are packed into `scales`. NT < kTerms
+// computes only the first NT terms (codes[t >= NT] and their scale bytes are 0).
+template <int NT = kTerms>
 __device__ __forceinline__ void split_block8(float v0, float v1, float v2, float v3,
                                              uint32_t codes[kTerms], uint32_t& scales) {
+  static_assert(NT >= 1 && NT <= kTerms, "1..kTerms terms");
   float r0 = v0, r1 = v1, r2 = v2, r3 = v3;
   scales = 0u;
 #pragma unroll
-  for (int t = 0; t < kTerms; ++t) {
+  for (int t = NT; t < kTerms; ++t) codes[t] = 0u;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
     const float m = max8(fmaxf(fmaxf(fabsf(r0), fabsf(r1)), fmaxf(fabsf(r2), fabsf(r3))));
     const int ex = (int)((__float_as_uint(m) >> 23) & 0xFFu);  // biased exponent; 0: zero/denormal
     const int sb = ex - 7;                                     // e8m0 byte of 2^(e-7)
