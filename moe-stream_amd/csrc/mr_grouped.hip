@@ -160,8 +160,9 @@ struct GroupedArgs {
 };
 
 // Grouped GEMM work item: (expert e, row tile, 32-pair tile); 4 waves. A wave owns kGT
-// 16-row A tiles of one matrix (gate/up: waves 0-1 gate, 2-3 up, the same 128 rows; down:
-// 4 x 64 = 256 rows) and the tile's 32 pairs as 2 groups of 16.
+// 16-row A tiles (gate/up: 32 gate rows and the same 32 up rows, so that the activation and the
+// split of the down input image run in registers, 128 rows per item; down: 4 x 64 = 256 rows)
+// and the tile's 32 pairs as 2 groups of 16.
 // The MFMAs take the first kGemmTerms = 3 e4m3 terms of the pairs' activation split (the
 // residual after three terms is below 2^-12 of each 32-element block's max, bf16 operands
 // hold 8 significant bits). A K step holds 4 weight blocks; MFMA m of the step takes term m of
@@ -250,8 +251,12 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
 
   const int nbK = a.K >> 5, S = (nbK + 3) >> 2;
   const uint64_t rb = (uint64_t)nbK * 17;
-  const int m = GATEUP ? (wave >> 1) : 0;
-  const int wrow0 = rt * kRows + (GATEUP ? (wave & 1) : wave) * (kGT * 16);
+  // Rows of this wave: gate/up: tiles 0 .. kTR-1 are the gate rows wrow0 .. wrow0 + 16 kTR - 1
+  // and tiles kTR .. 2kTR-1 the same up rows, so that a lane holds the gate and up values of
+  // the same (row, pair) for the activation; down: kGT tiles of consecutive rows.
+  constexpr int kTR = GATEUP ? kGT / 2 : kGT;  // 16-row tiles per matrix of a wave
+  static_assert(!GATEUP || kGT == 4, "gate/up: two gate and two up tiles, one 32-row split block per wave");
+  const int wrow0 = rt * kRows + wave * (kTR * 16);
   if (GATEUP) {  // read by the epilogue (after the K loop's barriers)
     for (int q = tid; q < 2 * kRows + kPairTile; q += kGW * 64) {
       if (q < 2 * kRows) {
@@ -263,14 +268,14 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
       }
     }
   }
-  const uint8_t* W = expert_at(m ? a.w1 : a.w0, e);
-  bool tin[kGT];  // tile inside the matrix (wave-uniform)
+  const uint8_t* Wm[2] = {expert_at(a.w0, e), GATEUP ? expert_at(a.w1, e) : expert_at(a.w0, e)};
+  // This lane's row i: its rows in every tile of one matrix are 16 rows (a multiple of 16
+  // bytes) apart, so the byte position of a block in its 16-byte piece is the same for all of
+  // them (lead0[matrix]; the gate and up matrices may start at different offsets).
+  uint32_t lead0[2];
 #pragma unroll
-  for (int tt = 0; tt < kGT; ++tt) tin[tt] = wrow0 + 16 * tt < a.M;
-  // This lane's row i: its rows in every tile are 16 rows (a multiple of 16 bytes) apart,
-  // so the byte position of a block in its 16-byte piece is the same for all of them.
-  const uintptr_t row_i = reinterpret_cast<uintptr_t>(W) + (uintptr_t)min(wrow0 + i, a.M - 1) * rb;
-  const uint32_t lead0 = (uint32_t)row_i & 15u;  // row start within its piece
+  for (int mt = 0; mt < 2; ++mt)
+    lead0[mt] = (uint32_t)(reinterpret_cast<uintptr_t>(Wm[mt]) + (uintptr_t)min(wrow0 + i, a.M - 1) * rb) & 15u;
   // A piece slots of this lane: slot k*64 + lane = (tile, row, piece) of the wave's rows
   const uint8_t* aps[kAK];
   int apc[kAK], aslot[kAK];
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     const int sl = min(k * 64 + lane, kASlots - 1);
     const int tt = sl / (16 * kAPR), rr = (sl / kAPR) % 16;
     apc[k] = sl % kAPR;
-    aps[k] = W + (uint64_t)min(wrow0 + 16 * tt + rr, a.M - 1) * rb;
+    aps[k] = Wm[tt / kTR] + (uint64_t)min(wrow0 + 16 * (tt % kTR) + rr, a.M - 1) * rb;
     aslot[k] = (tt * 16 + rr) * kARow + apc[k] * 16;
   }
 
@@ -385,7 +390,9 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
     load_a(min(st + 2, S - 1), cur);
     const uint8_t* bb_base = &bst[buf][0];
     const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(&bsc[buf][0]);
-    const uint32_t lead = (lead0 + 4u * (uint32_t)st) & 15u;  // 68 st = 4 st mod 16
+    uint32_t wo[2];  // per matrix: block g's scale byte in the row's LDS slice (68 st = 4 st mod 16)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) wo[mt] = ((lead0[mt] + 4u * (uint32_t)st) & 15u) + 17u * (uint32_t)g;
     // B operands of MFMA mm for the 2 pair groups, read one MFMA ahead; the A operands (this
     // lane's block g of each tile's row i) once per step for all three MFMAs. A block past the
     // row end (read inside the LDS stage) gets zero codes, so it adds nothing.
@@ -403,17 +410,15 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
         o.sb[pg] = (int)sc_base[sc_lane + mm + pg * 256];
       }
     };
-    const uint32_t wo = lead + 17u * (uint32_t)g;  // block g's scale byte in the row's LDS slice
     RawBlk r[kGT];
 #pragma unroll
     for (int tt = 0; tt < kGT; ++tt) {
-      const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo & ~3u)]);
+      const uint32_t* wp = reinterpret_cast<const uint32_t*>(&ast[wave][(tt * 16 + i) * kARow + (wo[tt / kTR] & ~3u)]);
       r[tt].d[0] = wp[0], r[tt].d[1] = wp[1], r[tt].d[2] = wp[2], r[tt].d[3] = wp[3], r[tt].d[4] = wp[4];
     }
     BOps o0, o1;
     read_b(0, o0);
     read_b(1, o1);
-    const uint32_t t = (wo & 3u) + 1u;  // the codes start t bytes into the window (1..4)
     const bool valid = !kPart || 4 * st + g < nbK;
     AOp ao[kGT];
     int sa[kGT];
@@ -422,12 +427,13 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
       // byte alignment by v_alignbyte (a shift of 4 bytes selects the upper dword): the same
       // as shifting the dword pair right by t bytes, which the compiler would otherwise do
       // through a stack copy of the window
+      const uint32_t w3 = wo[tt / kTR] & 3u, t = w3 + 1u;  // the codes start t bytes into the window (1..4)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t v = t == 4u ? r[tt].d[q + 1] : __builtin_amdgcn_alignbyte(r[tt].d[q + 1], r[tt].d[q], t);
         ao[tt].q[q] = valid ? v : 0u;
       }
-      sa[tt] = valid ? (int)((r[tt].d[0] >> (8u * (wo & 3u))) & 0xFFu) : 127;
+      sa[tt] = valid ? (int)((r[tt].d[0] >> (8u * w3)) & 0xFFu) : 127;
     }
     auto run_b = [&](const BOps& o) {
 #pragma unroll
@@ -470,55 +476,40 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
       }
     return;
   }
-  // Gate/up: the wave's block goes through LDS as [pair][row] so that each pair's rows are stored
-  // contiguously (and the up waves find the gate values of their rows there). Row rr of pair
-  // pl sits at rr ^ 4 (pl % 16) within the pair's kWR words: the 16 pairs of one write (a
-  // row stride of kWR = 64 words would put them all in one bank) spread over 16 bank groups.
-  __syncthreads();  // the K loop's LDS is no longer read
-  constexpr int kWR = kGT * 16;                                  // rows of a wave
-  constexpr int kSwz = (kWR >= 64 && (kWR & (kWR - 1)) == 0) ? 15 : 0;  // XOR stays inside kWR
-  auto at_pr = [&](int pl, int rr) { return pl * kWR + (rr ^ ((pl & kSwz) << 2)); };
-  float* blk = reinterpret_cast<float*>(&bst[0][0]) + wave * kPairTile * kWR;  // [pair][row]
+  // Gate/up: lane (i, g) holds gate rows 4g .. 4g+3 and 16+4g .. 16+4g+3 of the wave's 32
+  // rows (tiles 0, 1) and the same up rows (tiles 2, 3) for pairs i and 16 + i. h = act(gate +
+  // b_g, up + b_u) x routing weight is formed in registers and the wave's 32 rows of each pair,
+  // one block of the down input image, are split there: the lane holds split lanes 2g and 2g+1
+  // (elements 4g, 4g+16, 4g+1, 4g+17 and 4g+2, 4g+18, 4g+3, 4g+19; the split of k_split_rows),
+  // the block's other elements are in lanes xor 16 and xor 32.
+  const int lr0 = wave * (kTR * 16);  // the wave's first row within the item (bias_s index)
+  const int nbM = a.M >> 5;
 #pragma unroll
-  for (int tt = 0; tt < kGT; ++tt)
+  for (int pg = 0; pg < kPG; ++pg) {
+    const int pl = pg * 16 + i;
+    const float pw = bias_s[2 * kRows + min(pl, kPairTile - 1)];
+    float hv[2][4];  // [tile][r]: row 16 tile + 4g + r
 #pragma unroll
-    for (int pg = 0; pg < kPG; ++pg)
+    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) blk[at_pr(pg * 16 + i, tt * 16 + 4 * g + r)] = acc[tt][pg][r];
-  __syncthreads();
-  // h = act(gate, up) x routing weight over the gate values, by all four waves: the blocks
-  // of gate waves 0 and 1 then hold h of the tile rows 0 .. kWR-1 and kWR .. 2kWR-1 ([pair][row] each)
-  float* ldsf = reinterpret_cast<float*>(&bst[0][0]);
-  for (int q = tid; q < np * kRows; q += kGW * 64) {
-    const int pl = q / kRows, r = q - pl * kRows;
-    if (rt * kRows + r >= a.M) continue;
-    const int half = r >= kWR ? 1 : 0, at = half * kPairTile * kWR + at_pr(pl, r - half * kWR);
-    float gv = ldsf[at], uv = ldsf[2 * kPairTile * kWR + at];
-    if (a.b0) gv = gv + bias_s[r];
-    if (a.b1) uv = uv + bias_s[kRows + r];
-    const float h = a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
-    ldsf[at] = h * bias_s[2 * kRows + pl];
-  }
-  __syncthreads();
-  // each (pair, 32-row block) of the tile split into the down input image (the split of
-  // k_split_rows, 8 lanes per block: lane m8 takes elements 2m8, 2m8+16, 2m8+1, 2m8+17)
-  const float* hb = reinterpret_cast<const float*>(&bst[0][0]);
-  const int tr0 = rt * kRows, nbM = a.M >> 5;
-  const int nblk = min(kRows, a.M - tr0) >> 5;  // blocks of this tile (M % 32 == 0)
-  const int m8 = tid & 7;
-  auto hval = [&](int pl, int r) {  // h of tile row r (< kRows), pair pl
-    const int half = r >= kWR ? 1 : 0;
-    return hb[half * kPairTile * kWR + at_pr(pl, r - half * kWR)];
-  };
-  for (int u = tid >> 3; u < np * nblk; u += kGW * 8) {  // a whole 8-lane group per unit
-    const int pl = u / nblk, b = u - pl * nblk, r0 = 32 * b + 2 * m8;
-    uint32_t codes[kTerms], scales;
-    split_block8<kGemmTerms>(hval(pl, r0), hval(pl, r0 + 16), hval(pl, r0 + 1), hval(pl, r0 + 17), codes, scales);
-    const size_t bi = (size_t)(p0 + pl) * nbM + (tr0 >> 5) + b;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(a.himg + bi * kImgBytes);
+      for (int r = 0; r < 4; ++r) {
+        const int lr = lr0 + 16 * t2 + 4 * g + r;
+        float gv = acc[t2][pg][r], uv = acc[2 + t2][pg][r];
+        if (a.b0) gv = gv + bias_s[lr];
+        if (a.b1) uv = uv + bias_s[kRows + lr];
+        hv[t2][r] = (a.act == MR_ACT_SWIGLU_OAI ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv)) * pw;
+      }
+    uint32_t ca[kTerms], cb[kTerms], scales;
+    split_block_x2<kGemmTerms>(hv[0][0], hv[1][0], hv[0][1], hv[1][1], hv[0][2], hv[1][2], hv[0][3], hv[1][3], ca, cb,
+                               scales);
+    if (pl < np && wrow0 < a.M) {  // M % 32 == 0: the wave's 32 rows are all inside
+      const size_t bi = (size_t)(p0 + pl) * nbM + (wrow0 >> 5);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(a.himg + bi * kImgBytes);
 #pragma unroll
-    for (int t = 0; t < kGemmTerms; ++t) dst[t * 8 + m8] = codes[t];
-    if (m8 == 0) a.hsc[bi] = scales;
+      for (int t = 0; t < kGemmTerms; ++t)
+        *reinterpret_cast<uint2*>(dst + t * 8 + 2 * g) = make_uint2(ca[t], cb[t]);
+      if (g == 0) a.hsc[bi] = scales;
+    }
   }
 }
 

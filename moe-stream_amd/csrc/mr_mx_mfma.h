@@ -65,6 +65,45 @@ __device__ __forceinline__ void split_block8(float v0, float v1, float v2, float
   }
 }
 
+// The same split with the block's 32 elements in 4 lanes (this lane and the lanes xor 16 and
+// xor 32), each holding split lanes 2n and 2n+1: a0..a3 the elements of lane 2n, b0..b3 those
+// of lane 2n+1 (in the order of split_block8). ca/cb get the code dwords of both; the codes
+// and scales are the same bits as split_block8's for the same block.
+template <int NT = kTerms>
+__device__ __forceinline__ void split_block_x2(float a0, float a1, float a2, float a3, float b0, float b1, float b2,
+                                               float b3, uint32_t ca[kTerms], uint32_t cb[kTerms], uint32_t& scales) {
+  static_assert(NT >= 1 && NT <= kTerms, "1..kTerms terms");
+  scales = 0u;
+#pragma unroll
+  for (int t = NT; t < kTerms; ++t) ca[t] = cb[t] = 0u;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float m = fmaxf(fmaxf(fmaxf(fabsf(a0), fabsf(a1)), fmaxf(fabsf(a2), fabsf(a3))),
+                    fmaxf(fmaxf(fabsf(b0), fabsf(b1)), fmaxf(fabsf(b2), fabsf(b3))));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const int ex = (int)((__float_as_uint(m) >> 23) & 0xFFu);  // biased exponent; 0: zero/denormal
+    const int sb = ex - 7;                                     // e8m0 byte of 2^(e-7)
+    uint32_t c = 0u, d = 0u;
+    if (sb > 0) {
+      const float inv = __uint_as_float((uint32_t)(254 - sb) << 23);  // 2^-(e-7)
+      const float sc = __uint_as_float((uint32_t)sb << 23);           // 2^(e-7)
+      c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a0 * inv, a1 * inv, 0, false);
+      c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a2 * inv, a3 * inv, (int)c, true);
+      d = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(b0 * inv, b1 * inv, 0, false);
+      d = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(b2 * inv, b3 * inv, (int)d, true);
+      if (t + 1 < NT) {  // the residual feeds the next term
+        const f32x2 c01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c, false), c23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c, true);
+        const f32x2 d01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, false), d23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, true);
+        a0 -= c01.x * sc, a1 -= c01.y * sc, a2 -= c23.x * sc, a3 -= c23.y * sc;
+        b0 -= d01.x * sc, b1 -= d01.y * sc, b2 -= d23.x * sc, b3 -= d23.y * sc;
+      }
+      scales |= (uint32_t)sb << (8 * t);
+    }
+    ca[t] = c, cb[t] = d;
+  }
+}
+
 // ---- operands ----------------------------------------------------------------------------
 // B operand of lane (col i, group g) for K step st from a B image in LDS.
 // Columns i >= kTerms and blocks past nb read `zero` (32 zero bytes in LDS),
