@@ -485,6 +485,45 @@ def test_fused_scattered_expert_offsets(gpu_ctx, layers, name):
             b.free()
 
 
+@pytest.mark.parametrize("name", ["tiny-mxfp4", "C1-gpt-oss"])
+def test_grouped_packs_at_different_byte_offsets(gpu_ctx, layers, name):
+    """Grouped MXFP4 GEMMs (multi-token path) with the gate, up and down experts starting 0, 8
+    and 4 bytes further into their 16-byte pieces than in the contiguous packs (one gate/up
+    work item reads gate and up rows, each at its own offset): the same bits as the contiguous
+    packs."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    H, I, E, t = spec.hidden, spec.inter, spec.n_experts, spec.ggml_type
+
+    def shifted(data, out_f, in_f, shift):
+        mb = data.nbytes // E
+        step = mb + 256
+        buf = np.zeros(E * step + 16, np.uint8)
+        offs = [(E - 1 - e) * step + shift for e in range(E)]
+        for e, o in enumerate(offs):
+            buf[o:o + mb] = data[e * mb:(e + 1) * mb]
+        return M.ExpertPack.upload(gpu_ctx, t, buf, E, out_f, in_f, offsets=offs)
+
+    packs = [shifted(host["gate"], I, H, 0), shifted(host["up"], I, H, 8), shifted(host["down"], H, I, 4)]
+    L = M.MoeLayer(gpu_ctx, *packs, router_w=dl.f["router_w"], router_b=dl.f["router_b"],
+                   gate_bias=dl.f["gate_b"], up_bias=dl.f["up_b"], down_bias=dl.f["down_b"],
+                   top_k=spec.top_k, route_flags=spec.route_flags, act=spec.act, alpha=spec.alpha,
+                   limit=spec.limit)
+    T = 45
+    x = W.x_tokens(spec, T, first_token=90)
+    dx, y1, y2 = gpu_ctx.to_device(x), gpu_ctx.alloc(T * H * 4), gpu_ctx.alloc(T * H * 4)
+    try:
+        dl.layer.forward_batched(dx, T, y1)
+        L.forward_batched(dx, T, y2)
+        assert np.array_equal(y1.download(np.float32), y2.download(np.float32))
+    finally:
+        L.close()
+        for p in packs:
+            p.close()
+        for b in (dx, y1, y2):
+            b.free()
+
+
 @pytest.mark.parametrize("name", ["tiny-mxfp4", "tiny-q4k-shared"])
 def test_fused_graph_replay(gpu_ctx, layers, name):
     dl, _ = get_layer(gpu_ctx, layers, name)
