@@ -177,9 +177,9 @@ struct GroupedArgs {
 //      load covers ~11 rows' contiguous bytes; 20-byte windows loaded per lane straight
 //      from global cost 3x the L1 accesses), two steps ahead in registers, then written to
 //      the wave's LDS slice, from which the 4 lanes of a row read the same block window;
-//   B: the step's 32 pairs x 4 blocks x 128-byte images (16 KB) and their scale words, two
-//      steps ahead in registers (4 pieces per thread), then written to a double-buffered LDS
-//      stage shared by the 4 waves. (Direct global->LDS loads would save the registers, but
+//   B: the step's 32 pairs x 4 blocks x the 96 bytes of terms 0-2 of their images (12 KB) and
+//      their scale words, one step ahead in registers (3 pieces per thread; the images are L2
+//      hits), then written to a double-buffered LDS stage shared by the 4 waves. (Direct global->LDS loads would save the registers, but
 //      the compiler then waits for all of them before any LDS read, which serialises the
 //      prefetch.) 16-byte part q of (pair pr, block b) sits in slot b_slot(pr, b, q),
 //      so the 16 lanes of a read (16 pairs, one part) hit 16 different bank groups.
