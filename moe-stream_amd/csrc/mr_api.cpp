@@ -123,7 +123,7 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40 + (k + 1) * H * 4 + 256);
   p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
-  p.grouped = o, o += align_up(std::max(mr::grouped_scratch_bytes(T, k, E, I, H),
+  p.grouped = o, o += align_up(std::max(mr::grouped_scratch_bytes(T, k, E, I, H, Ish),
                                         mr::grouped_q4k_scratch_bytes(T, k, E, I, H, Ish)));
   p.xn = o, o += align_up(T * H * 4);
   p.ytmp = o, o += align_up(T * H * 4);
@@ -156,7 +156,7 @@ BatchedPlan plan_batched(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.rpart = o, o += align_up(4 * T * E * 4);
   p.work = o;
   if (kind == Batched::grouped_mx) {
-    o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H));
+    o += align_up(mr::grouped_scratch_bytes(T, k, E, I, H, Ish));
     p.work_sh = o;
   } else if (kind == Batched::grouped_q4k) {
     o += align_up(mr::grouped_q4k_scratch_bytes(T, k, E, I, H, Ish));
@@ -809,7 +809,7 @@ static hipError_t batched_core(mr_ctx* c, const mr_layer* L, const float* x, uin
     const Batched kind = batched_kind(c, *L);
     if (kind == Batched::grouped_mx)
       e = mr::launch_grouped(c->launch(), *L, x, T, s.idx, s.w, y,
-                             mr::grouped_scratch(s, s.cap_tokens, s.cap_k, s.cap_e, s.cap_i, s.cap_h));
+                             mr::grouped_scratch(s, s.cap_tokens, s.cap_k, s.cap_e, s.cap_i, s.cap_h, s.cap_ish));
     else if (kind == Batched::grouped_q4k)
       e = mr::launch_grouped_q4k(c->launch(), *L, x, T, s.idx, s.w, y, s.grouped);
     else
@@ -886,7 +886,7 @@ int mr_moe_forward_batched_noalloc(mr_ctx* c, const mr_layer* L, const float* x,
       mr::Scratch view{};
       view.grouped = b + p.work;
       e = mr::launch_grouped(K, *L, x, T, idx, w, y,
-                             mr::grouped_scratch(view, T, L->d.top_k, L->E, L->I, L->H));
+                             mr::grouped_scratch(view, T, L->d.top_k, L->E, L->I, L->H, L->Ish));
     } else if (kind == Batched::grouped_q4k) {
       e = mr::launch_grouped_q4k(K, *L, x, T, idx, w, y, b + p.work);
     } else {

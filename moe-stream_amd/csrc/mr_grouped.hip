@@ -148,9 +148,11 @@ struct GroupedArgs {
   const uint8_t* img;    // B images [rows][K/32][kImgBytes]
   const uint32_t* isc;   // [rows][K/32]
   const int32_t* pair_tok;  // B row of pair p (GATEUP: its token) or null (row = p)
-  const float* pair_w;
+  const float* pair_w;      // GATEUP: routing weight of pair p, or null (weight 1)
   const int32_t* exp_off;
   const int32_t* tile_off;
+  int single_p;  // > 0: one expert (e = 0) over pairs 0 .. single_p - 1 (the shared expert over
+                 // every token); exp_off and tile_off are not read
   float* out;        // [P][M] (down)
   uint8_t* himg;     // GATEUP: the down input images [P][M/32][kImgBytes]
   uint32_t* hsc;     // GATEUP: their scale words [P][M/32]
@@ -231,22 +233,25 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
   // the items that share an expert's row tile (A) or its pairs' images (B) run on the same
   // XCD and meet in its L2.
   const int n_rt = (a.M + kRows - 1) / kRows;
-  const int n_work = n_rt * a.tile_off[a.E];
+  const bool single = a.single_p > 0;
+  const int n_tiles = single ? (a.single_p + kPairTile - 1) / kPairTile : a.tile_off[a.E];
+  const int n_work = n_rt * n_tiles;
   const int per_xcd = (n_work + kXcds - 1) / kXcds;
   const int loc = blockIdx.x / kXcds;
   const int w = (blockIdx.x % kXcds) * per_xcd + loc;
   if (loc >= per_xcd || w >= n_work) return;  // uniform: no work item for this workgroup
-  int lo = 0, hi = a.E;  // expert: n_rt * tile_off[e] <= w < n_rt * tile_off[e+1]
+  int lo = 0, hi = single ? 1 : a.E;  // expert: n_rt * tile_off[e] <= w < n_rt * tile_off[e+1]
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (n_rt * a.tile_off[mid] <= w) lo = mid; else hi = mid;
   }
   const int e = lo;
-  const int nt_e = a.tile_off[e + 1] - a.tile_off[e];
-  const int wl = w - n_rt * a.tile_off[e];
+  const int e_beg = single ? 0 : a.exp_off[e], e_end = single ? a.single_p : a.exp_off[e + 1];
+  const int nt_e = single ? n_tiles : a.tile_off[e + 1] - a.tile_off[e];
+  const int wl = w - (single ? 0 : n_rt * a.tile_off[e]);
   const int rt = wl / nt_e, tl = wl - rt * nt_e;
-  const int p0 = a.exp_off[e] + tl * kPairTile;
-  const int np = min(kPairTile, a.exp_off[e + 1] - p0);
+  const int p0 = e_beg + tl * kPairTile;
+  const int np = min(kPairTile, e_end - p0);
   const int npg = (np + 15) >> 4;  // pair groups holding pairs (uniform)
 
   const int nbK = a.K >> 5, S = (nbK + 3) >> 2;
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void k_grouped_gemm(GroupedArgs a) {
         const float* bsrc = mat ? a.b1 : a.b0;
         bias_s[q] = (bsrc && orow < a.M) ? bsrc[(size_t)e * a.M + orow] : 0.f;
       } else {
-        bias_s[q] = a.pair_w[p0 + min(q - 2 * kRows, np - 1)];
+        bias_s[q] = a.pair_w ? a.pair_w[p0 + min(q - 2 * kRows, np - 1)] : 1.f;
       }
     }
   }
@@ -580,9 +585,10 @@ namespace {
 constexpr uint64_t kAlign = 256;
 uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct GroupedPlan {
-  uint64_t pair_tok, pair_w, pair_of, exp_off, tile_off, img_x, sc_x, img_h, sc_h, obuf, total;
+  uint64_t pair_tok, pair_w, pair_of, exp_off, tile_off, img_x, sc_x, img_h, sc_h, obuf;
+  uint64_t img_hsh, sc_hsh, osh, sig, total;
 };
-GroupedPlan grouped_plan(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H) {
+GroupedPlan grouped_plan(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
   GroupedPlan p{};
   const uint64_t P = T * k;
   uint64_t o = 0;
@@ -596,17 +602,22 @@ GroupedPlan grouped_plan(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.img_h = o, o += up(P * (I / 32) * kImgBytes);
   p.sc_h = o, o += up(P * (I / 32) * 4);
   p.obuf = o, o += up(P * H * 4);
+  p.img_hsh = o, o += up(T * (Ish / 32) * kImgBytes);  // the shared expert (Ish = 0: none)
+  p.sc_hsh = o, o += up(T * (Ish / 32) * 4);
+  p.osh = o, o += up(Ish ? T * H * 4 : 0);
+  p.sig = o, o += up(Ish ? T * 4 : 0);
   p.total = o;
   return p;
 }
 }  // namespace
 
-uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H) {
-  return grouped_plan(T, k, E, I, H).total;
+uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish) {
+  return grouped_plan(T, k, E, I, H, Ish).total;
 }
 
-GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H) {
-  const GroupedPlan p = grouped_plan(T, k, E, I, H);
+GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H,
+                               uint64_t Ish) {
+  const GroupedPlan p = grouped_plan(T, k, E, I, H, Ish);
   char* b = static_cast<char*>(s.grouped);
   GroupedScratch g{};
   g.pair_tok = reinterpret_cast<int32_t*>(b + p.pair_tok);
@@ -619,11 +630,23 @@ GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_
   g.img_h = reinterpret_cast<uint8_t*>(b + p.img_h);
   g.sc_h = reinterpret_cast<uint32_t*>(b + p.sc_h);
   g.obuf = reinterpret_cast<float*>(b + p.obuf);
+  g.img_hsh = reinterpret_cast<uint8_t*>(b + p.img_hsh);
+  g.sc_hsh = reinterpret_cast<uint32_t*>(b + p.sc_hsh);
+  g.osh = reinterpret_cast<float*>(b + p.osh);
+  g.sig = reinterpret_cast<float*>(b + p.sig);
   return g;
 }
+// MXFP4 routed experts, and an MXFP4 shared expert of any width (a multiple of 32), which runs
+// as one more group: every token, weight 1, SiLU, then its sigmoid gate in the combine.
 bool grouped_supported(const mr_layer& L) {
-  return L.type == MR_GGML_MXFP4 && !L.d.sh_gate && L.d.top_k <= 16 && L.H % 32 == 0 && L.I % 32 == 0 &&
-         L.E <= 1024 && L.H <= 4u * 32 * kMaxSteps && L.I <= 4u * 32 * kMaxSteps;
+  if (L.type != MR_GGML_MXFP4 || L.d.top_k > 16 || L.H % 32 != 0 || L.I % 32 != 0 || L.E > 1024 ||
+      L.H > 4u * 32 * kMaxSteps || L.I > 4u * 32 * kMaxSteps)
+    return false;
+  if (L.d.sh_gate && (L.d.sh_gate->type != MR_GGML_MXFP4 || L.d.sh_up->type != MR_GGML_MXFP4 ||
+                      L.d.sh_down->type != MR_GGML_MXFP4 || L.Ish == 0 || L.Ish % 32 != 0 ||
+                      L.Ish > 4u * 32 * kMaxSteps))
+    return false;
+  return true;
 }
 
 hipError_t launch_group(const Launch& K, const int32_t* idx, const float* w, int P, int k, int E, int32_t* pair_tok,
@@ -697,7 +720,37 @@ hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, ui
                        K.s, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  return launch_combine(K, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, T, k, H, nullptr, nullptr, y);
+  if (!L.d.sh_gate) return launch_combine(K, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, T, k, H, nullptr, nullptr, y);
+  // The shared expert (layer.rs:1898-1953): one group of every token on the same x images,
+  // weight 1 and SiLU (the routed experts' activation does not apply), its down outputs
+  // [T][H], then sigmoid(x . gate_inp) per token, which the combine applies after the routed
+  // sum.
+  const int Ish = (int)L.Ish, tiles = ((int)T + kPairTile - 1) / kPairTile;
+  GroupedArgs sg{};
+  sg.w0 = expert_loc(L.d.sh_gate), sg.w1 = expert_loc(L.d.sh_up);
+  sg.img = gs.img_x, sg.isc = gs.sc_x, sg.single_p = (int)T;
+  sg.himg = gs.img_hsh, sg.hsc = gs.sc_hsh;
+  sg.M = Ish, sg.K = H, sg.E = 1, sg.act = MR_ACT_SILU;
+  {
+    ProfScope ps(K, "grouped_shared_gateup");
+    constexpr int rows = kRowsOf<true>;
+    hipLaunchKernelGGL(k_grouped_gemm<true>, dim3(grouped_grid((uint64_t)((Ish + rows - 1) / rows) * tiles)),
+                       dim3(kGW * 64), 0, K.s, sg);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  GroupedArgs sd{};
+  sd.w0 = expert_loc(L.d.sh_down);
+  sd.img = gs.img_hsh, sd.isc = gs.sc_hsh, sd.single_p = (int)T, sd.out = gs.osh;
+  sd.M = H, sd.K = Ish, sd.E = 1;
+  {
+    ProfScope ps(K, "grouped_shared_down");
+    constexpr int rows = kRowsOf<false>;
+    hipLaunchKernelGGL(k_grouped_gemm<false>, dim3(grouped_grid((uint64_t)((H + rows - 1) / rows) * tiles)),
+                       dim3(kGW * 64), 0, K.s, sd);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if ((e = launch_sh_gate(K, x, T, H, L.d.sh_gate_inp, gs.sig)) != hipSuccess) return e;
+  return launch_combine(K, gs.obuf, gs.pair_of, idx, w, L.d.down_bias, T, k, H, gs.osh, gs.sig, y);
 }
 
 }  // namespace mr

@@ -424,6 +424,12 @@ uint64_t grouped_q4k_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t 
   return q4_plan(T, k, E, I, H, Ish).total;
 }
 
+hipError_t launch_sh_gate(const Launch& K, const float* x, uint32_t T, int H, const float* gate_inp, float* sig) {
+  ProfScope ps(K, "shared_gate");
+  hipLaunchKernelGGL(k_sh_gate, dim3(T), dim3(64), 0, K.s, x, H, gate_inp, sig);
+  return hipGetLastError();
+}
+
 // Q4_K routed experts (and a Q4_K shared expert) with K dimensions in whole super-blocks.
 bool grouped_q4k_supported(const mr_layer& L) {
   if (L.type != MR_GGML_Q4_K || L.d.top_k > 16 || L.E > 1024) return false;
@@ -498,11 +504,7 @@ hipError_t launch_grouped_q4k(const Launch& K, const mr_layer& L, const float* x
       hipLaunchKernelGGL(k_grouped_q4k<false>, dim3(grouped_grid((uint64_t)((H + 63) / 64) * tiles)), dim3(256), 0, K.s, sd);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    {
-      ProfScope ps(K, "shared_gate");
-      hipLaunchKernelGGL(k_sh_gate, dim3(T), dim3(64), 0, K.s, x, H, L.d.sh_gate_inp, sig);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
+    if ((e = launch_sh_gate(K, x, T, H, L.d.sh_gate_inp, sig)) != hipSuccess) return e;
   }
   return launch_combine(K, o, pair_of, idx, w, L.d.down_bias, T, k, H, osh, sig, y);
 }

@@ -237,9 +237,16 @@ struct GroupedScratch {
   uint8_t* img_h;     // [P][I/32][128] h images
   uint32_t* sc_h;     // [P][I/32]
   float* obuf;        // [P][H] down results
+  uint8_t* img_hsh;   // [T][Ish/32][128] shared-expert h images
+  uint32_t* sc_hsh;   // [T][Ish/32]
+  float* osh;         // [T][H] shared-expert down results
+  float* sig;         // [T] its sigmoid gate
 };
-GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H);
-uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H);
+GroupedScratch grouped_scratch(const Scratch& s, uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H,
+                               uint64_t Ish);
+uint64_t grouped_scratch_bytes(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_t H, uint64_t Ish);
+// sigmoid(x_t . gate_inp) per token t, or 1 without gate_inp (mr_grouped_q4k.hip)
+hipError_t launch_sh_gate(const Launch& K, const float* x, uint32_t T, int H, const float* gate_inp, float* sig);
 bool grouped_supported(const mr_layer& L);
 hipError_t launch_grouped(const Launch& K, const mr_layer& L, const float* x, uint32_t T, const int32_t* idx,
                           const float* w, float* y, const GroupedScratch& gs);

@@ -131,9 +131,18 @@ WIDE_MX = {
     "mxfp4-k6-shared-H2880": W.LayerSpec(221, 0, W.GGML_MXFP4, 2880, 1536, 64, 6, W.ROUTE_NORM_TOPK,
                                          W.ACT_SWIGLU_OAI, True, True, sh_inter=1536, sh_type=W.GGML_MXFP4),
 }
+# An MXFP4 shared expert four times as wide as the routed experts (the Qwen2-MoE proportion): the
+# fused decode kernel declines it (the shared slot would need more units than a routed one);
+# decode takes the multi-kernel path, batches the grouped GEMMs with the shared expert as one
+# more group.
+WIDE_SH = {
+    "mxfp4-k4-shared-x4": W.LayerSpec(222, 0, W.GGML_MXFP4, 1024, 256, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                      False, False, sh_inter=1024, sh_type=W.GGML_MXFP4),
+}
 SPECS = {
     **WIDE_Q4,
     **WIDE_MX,
+    **WIDE_SH,
     "tiny-mxfp4": TINY_MX,
     "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
@@ -333,6 +342,46 @@ def test_grouped_batched_many_tokens(gpu_ctx, layers):
         if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg[n]).max():
             assert rel_err(y[t], ry[n]) <= REL_TOL, (t, rel_err(y[t], ry[n]))
     for b in (dx, dy, dv, di, dw, dlg):
+        b.free()
+
+
+@pytest.mark.parametrize("name,T", [("mxfp4-k4-shared", 37), ("mxfp4-k16-shared", 40), ("mxfp4-k3-shared", 1),
+                                    ("mxfp4-k6-shared-H2880", 70), ("mxfp4-k4-shared-x4", 33)])
+def test_grouped_shared_expert_parity(gpu_ctx, layers, name, T):
+    """Multi-token MXFP4 layers with an MXFP4 shared expert: the grouped GEMMs run the shared
+    expert as one group of every token (weight 1, SiLU) and the combine adds it, sigmoid-gated,
+    after the routed sum (layer.rs:1898-1953). Per token against the oracle and the VALU path."""
+    dl, host = get_layer(gpu_ctx, layers, name)
+    spec = dl.spec
+    x = W.x_tokens(spec, T, first_token=400)
+    dx = gpu_ctx.to_device(x)
+    dy, dv = gpu_ctx.alloc(T * spec.hidden * 4), gpu_ctx.alloc(T * spec.hidden * 4)
+    gpu_ctx.profile_reset()
+    gpu_ctx.set_option(M.OPT_PROFILE, 1)
+    try:
+        dl.layer.forward_batched(dx, T, dy)
+        n_sh = gpu_ctx.profile_read("grouped_shared_gateup")[0]
+        n_gu = gpu_ctx.profile_read("grouped_gateup")[0]
+    finally:
+        gpu_ctx.set_option(M.OPT_PROFILE, 0)
+    assert (n_sh, n_gu) == (1, 1), "the grouped MXFP4 kernels did not run"
+    gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_VALU)
+    try:
+        dl.layer.forward_batched(dx, T, dv)
+    finally:
+        gpu_ctx.set_option(M.OPT_DECODE_KERNEL, M.DECODE_AUTO)
+    y = dy.download(np.float32).reshape(T, -1)
+    yv = dv.download(np.float32).reshape(T, -1)
+    ry, _, _, rlg = oracle.layer_from_host(host).forward(x, n_threads=8)
+    checked = 0
+    for t in range(T):
+        s = np.sort(rlg[t])[::-1]
+        if s[spec.top_k - 1] - s[spec.top_k] > 1e-5 * np.abs(rlg[t]).max():
+            assert rel_err(y[t], ry[t]) <= REL_TOL, (t, rel_err(y[t], ry[t]))
+            assert rel_err(y[t], yv[t]) <= 2 * REL_TOL, (t, rel_err(y[t], yv[t]))
+            checked += 1
+    assert checked >= max(1, T - 2)
+    for b in (dx, dy, dv):
         b.free()
 
 
