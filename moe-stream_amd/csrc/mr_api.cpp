@@ -117,10 +117,10 @@ ScratchPlan plan_scratch(uint64_t T, uint64_t k, uint64_t E, uint64_t I, uint64_
   p.rpart = o, o += align_up(4 * T * E * 4);
   p.act = o, o += align_up(T * k * I * 4);
   p.act_sh = o, o += align_up(T * (Ish + 1) * 4);
-  // MFMA B-operand images: x split (H/32 blocks) and act split (k*I/32 blocks),
-  // 16 columns x 33 bytes per block, rounded generously; then the fused MXFP4 kernel's
-  // per-slot down rows (top_k + shared slots of H floats).
-  p.mfma_b = o, o += align_up(((H / 32) + (k * I / 32) + 64) * 16 * 40 + (k + 1) * H * 4 + 256);
+  // MFMA B-operand images: x split (H/32 blocks) and act split (k*I/32 blocks, then Ish/32 of
+  // the shared expert), 16 columns x 33 bytes per block, rounded generously; then the fused
+  // MXFP4 kernel's per-slot down rows (top_k + shared slots of H floats).
+  p.mfma_b = o, o += align_up(((H / 32) + ((k * I + Ish) / 32) + 64) * 16 * 40 + (k + 1) * H * 4 + 256);
   p.sync = o, o += align_up(4096);
   p.groups = o, o += align_up((T * k + E + 64) * 8);
   p.grouped = o, o += align_up(std::max(mr::grouped_scratch_bytes(T, k, E, I, H, Ish),

@@ -76,10 +76,11 @@ struct FusedArgs {
   const uint8_t* sh_up;
   const uint8_t* sh_down;
   const float* sh_gate_inp;
-  uint8_t* dimg;  // [ktot][nbI][kImgBytes] down B image
-  uint32_t* dsc;  // [ktot][nbI] 4 e8m0 bytes (one per term)
+  uint8_t* dimg;  // [k * nbI + nbIsh][kImgBytes] down B image: routed slots, then the shared expert
+  uint32_t* dsc;  // [k * nbI + nbIsh] 4 e8m0 bytes (one per term)
   float* dpart;   // [ktot][H] down rows of each slot (more than four slots: combined by the last slot group)
   int H, I, E, k, ktot, has_sh;
+  int Ish;  // shared expert width (a multiple of 32, at most 32 * 4 * kSteps; 0 without one)
   uint32_t flags;
   int act;
   float alpha, limit;
@@ -439,8 +440,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     __syncthreads();  // selection and x image ready
     TRACE(2);
     if (ok_flag && gid < a.NG) {  // one unit per workgroup
-      const int unit = gid;
-      const int slot = unit / nrp, pair = unit % nrp;
+      // units 0 .. k*nrp-1: routed slot unit / nrp; then the shared expert's Ish/32 units
+      const int unit = gid, nru = a.k * nrp;
+      const bool routed_u = !GEN || unit < nru;  // !GEN: no shared expert, every unit is routed
+      const int slot = routed_u ? unit / nrp : a.k, pair = routed_u ? unit % nrp : unit - nru;
       const bool sh = slot >= a.k;  // the shared expert
       const int e = sh ? 0 : sel_i[slot];
       const int tile = wave & 1, mat = wave >> 1;  // mat 0: gate, 1: up
@@ -524,17 +527,20 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     TRACE(1);
     float yres = 0.f, ybias = 0.f;  // this thread's output-row residual and bias terms (tid < 16)
     if (ok_flag) {
-      const int S = (nbI + 3) >> 2;
       const int row = q * 16 + (half == 0 ? i : (half == 2 ? 8 : 0) + (i & 7));
-      const uint64_t rb = (uint64_t)nbI * 17;
       RawBlk rd[kSteps];
       const int slot = sg * 4 + wave;  // this wave's slot (routed, then the shared expert)
       const int sl = min(slot, ktot - 1);
+      // the slot's K blocks: I/32, or Ish/32 for the shared expert (its image follows the routed
+      // slots' images, so slot s's image starts at block s * nbI either way)
+      const int nbs = (GEN && sl >= a.k) ? (a.Ish >> 5) : nbI;
+      const int S = (nbs + 3) >> 2;
+      const uint64_t rb = (uint64_t)nbs * 17;
       const uint8_t* D = (sl >= a.k ? a.sh_down : expert_at(a.down, sel_i[sl])) + (uint64_t)row * rb;
       // the prefetch waits a while: issued at once, its bytes share HBM with the gate/up
       // streams from the start and delay the last gate/up units, which set the hand-off
       for (int it = 0; it < a.dn_delay; ++it) __builtin_amdgcn_s_sleep(8);
-      if (slot < ktot) issue_rows(D, S, nbI, g, rd);  // prefetch, independent of gate/up
+      if (slot < ktot) issue_rows(D, S, nbs, g, rd);  // prefetch, independent of gate/up
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
       // the combine order in registers (top_k <= 4), so the combine does no dependent LDS reads
       int so[4] = {0, 0, 0, 0};
@@ -547,7 +553,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       if (tid < 16 && a.down_b)
         for (int s2 = 0; s2 < a.k; ++s2) ybias = ybias + sel_w[s2] * a.down_b[(size_t)sel_i[s2] * a.H + q * 16 + tid];
       if (slot < ktot)  // waits for the weights: they land long before gate/up ends
-        prep_rows(rd, (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u, nbI, g);
+        prep_rows(rd, (uint32_t)reinterpret_cast<uintptr_t>(D) & 3u, nbs, g);
       TRACE(2);
       // polled every 4 sleep units once at most an eighth of the units are missing (+0.3%)
       if (wave == 0 &&
@@ -562,7 +568,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         if (slot < ktot) {
           {  // slot image -> LDS with direct global->LDS loads (no VGPRs in flight)
             const uint8_t* src = a.dimg + (size_t)slot * nbI * kImgBytes;
-            const int n16 = nbI * kImgBytes / 16;
+            const int n16 = nbs * kImgBytes / 16;
 #pragma unroll
             for (int jj = 0; jj < kImgVec; ++jj) {
               if (64 * jj < n16) {
@@ -570,17 +576,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
                 __builtin_amdgcn_global_load_lds(src + (size_t)idx * 16, wimg + 1024 * jj, 16, 0, 16 /* sc1 */);
               }
             }
-            const uint32_t sc0 = ld_sc1(a.dsc + slot * nbI + min(lane, nbI - 1));
-            const uint32_t sc1v = ld_sc1(a.dsc + slot * nbI + min(lane + 64, nbI - 1));
-            if (lane < nbI) wsc[lane] = sc0;
-            if (lane + 64 < nbI) wsc[lane + 64] = sc1v;
+            const uint32_t sc0 = ld_sc1(a.dsc + slot * nbI + min(lane, nbs - 1));
+            const uint32_t sc1v = ld_sc1(a.dsc + slot * nbI + min(lane + 64, nbs - 1));
+            if (lane < nbs) wsc[lane] = sc0;
+            if (lane + 64 < nbs) wsc[lane + 64] = sc1v;
             vm_drain();  // the slot image has landed in LDS
-            // blocks nbI .. 4*kSteps-1 (read by the last steps, which have all-zero A) and
+            // blocks nbs .. 4*kSteps-1 (read by the last steps, which have all-zero A) and
             // their scale words are zero; after the drain: the last direct load also wrote
             // copies of the final piece there
-            for (int z = lane; z < (4 * kSteps - nbI) * (kImgBytes / 16); z += 64)
-              reinterpret_cast<i32x4*>(wimg + (size_t)nbI * kImgBytes)[z] = i32x4{0, 0, 0, 0};
-            for (int z = nbI + lane; z < 4 * kSteps; z += 64) wsc[z] = 0u;
+            for (int z = lane; z < (4 * kSteps - nbs) * (kImgBytes / 16); z += 64)
+              reinterpret_cast<i32x4*>(wimg + (size_t)nbs * kImgBytes)[z] = i32x4{0, 0, 0, 0};
+            for (int z = nbs + lane; z < 4 * kSteps; z += 64) wsc[z] = 0u;
             __builtin_amdgcn_wave_barrier();
           }
           TRACE(4);
@@ -663,11 +669,12 @@ bool fused_supported(const mr_layer& L, int n_cu) {
   if (L.type != MR_GGML_MXFP4 || L.d.top_k > 16) return false;
   const uint64_t has_sh = L.d.sh_gate ? 1u : 0u;
   if (has_sh && (L.d.sh_gate->type != MR_GGML_MXFP4 || L.d.sh_up->type != MR_GGML_MXFP4 ||
-                 L.d.sh_down->type != MR_GGML_MXFP4 || L.Ish != L.I))
-    return false;  // a shared expert: MXFP4 like the routed ones, and as wide
+                 L.d.sh_down->type != MR_GGML_MXFP4 || L.Ish % 32 != 0 || L.Ish == 0 ||
+                 L.Ish > 32u * 4 * kSteps))
+    return false;  // a shared expert: MXFP4 like the routed ones, its K steps within a down wave's
   if (L.E + has_sh > (uint64_t)kMaxLogits) return false;
   const uint64_t ktot = L.d.top_k + has_sh, nsl = (ktot + 3) / 4;
-  const uint64_t R = (L.E + has_sh + 3) / 4, ND = (L.H + 15) / 16 * nsl, NG = ktot * (L.I / 32);
+  const uint64_t R = (L.E + has_sh + 3) / 4, ND = (L.H + 15) / 16 * nsl, NG = L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32);
   if (!fused_multi(L) && R + ND >= (uint64_t)n_cu) return false;  // routers and down groups in one dispatch round
   if (R + ND + NG > 3ull * n_cu) return false;
   if (R + ND + NG > (uint64_t)kMaxGrid) return false;  // the split groups are added only where they fit
@@ -696,7 +703,7 @@ static FusedGrid fused_grid(const mr_layer& L, int n_cu) {
   FusedGrid g;
   const uint32_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + has_sh;
   g.R = (int)((L.E + has_sh + 3) / 4);
-  g.NG = (int)(ktot * (L.I / 32));
+  g.NG = (int)(L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32));
   g.NDR = (int)((L.H + 15) / 16);
   g.nsl = (int)((ktot + 3) / 4);
   g.ND = g.NDR * g.nsl;
@@ -783,8 +790,10 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.logits_out = L.logits_out;
   const uint64_t nbH = L.H / 32, nbI = L.I / 32, k = L.d.top_k, ktot = k + (uint64_t)a.has_sh;
   a.dimg = img_base;
-  a.dsc = reinterpret_cast<uint32_t*>(img_base + ktot * nbI * kImgBytes);
-  a.dpart = reinterpret_cast<float*>(img_base + ((ktot * nbI * (kImgBytes + 4) + 255) & ~(uint64_t)255));
+  const uint64_t nblk = k * nbI + (a.has_sh ? L.Ish / 32 : 0);  // image blocks of every slot
+  a.dsc = reinterpret_cast<uint32_t*>(img_base + nblk * kImgBytes);
+  a.dpart = reinterpret_cast<float*>(img_base + ((nblk * (kImgBytes + 4) + 255) & ~(uint64_t)255));
+  a.Ish = a.has_sh ? (int)L.Ish : 0;
   a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k, a.ktot = (int)ktot;
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   const FusedGrid fg = fused_grid(L, n_cu);

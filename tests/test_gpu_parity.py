@@ -131,13 +131,15 @@ WIDE_MX = {
     "mxfp4-k6-shared-H2880": W.LayerSpec(221, 0, W.GGML_MXFP4, 2880, 1536, 64, 6, W.ROUTE_NORM_TOPK,
                                          W.ACT_SWIGLU_OAI, True, True, sh_inter=1536, sh_type=W.GGML_MXFP4),
 }
-# An MXFP4 shared expert four times as wide as the routed experts (the Qwen2-MoE proportion): the
-# fused decode kernel declines it (the shared slot would need more units than a routed one);
-# decode takes the multi-kernel path, batches the grouped GEMMs with the shared expert as one
-# more group.
+# MXFP4 shared experts wider than the routed experts (4x: the Qwen2-MoE proportion; 2944, the widest a
+# fused down wave takes: 23 K steps of 4 blocks): the
+# fused decode kernel gives the shared slot Ish/32 gate/up units and its down wave Ish/32 K blocks;
+# batches run the grouped GEMMs with the shared expert as one more group.
 WIDE_SH = {
     "mxfp4-k4-shared-x4": W.LayerSpec(222, 0, W.GGML_MXFP4, 1024, 256, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU,
                                       False, False, sh_inter=1024, sh_type=W.GGML_MXFP4),
+    "mxfp4-k8-shared-2944": W.LayerSpec(223, 0, W.GGML_MXFP4, 2048, 384, 64, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                        False, False, sh_inter=2944, sh_type=W.GGML_MXFP4),
 }
 SPECS = {
     **WIDE_Q4,
@@ -346,7 +348,8 @@ def test_grouped_batched_many_tokens(gpu_ctx, layers):
 
 
 @pytest.mark.parametrize("name,T", [("mxfp4-k4-shared", 37), ("mxfp4-k16-shared", 40), ("mxfp4-k3-shared", 1),
-                                    ("mxfp4-k6-shared-H2880", 70), ("mxfp4-k4-shared-x4", 33)])
+                                    ("mxfp4-k6-shared-H2880", 70), ("mxfp4-k4-shared-x4", 33),
+                                    ("mxfp4-k8-shared-2944", 24)])
 def test_grouped_shared_expert_parity(gpu_ctx, layers, name, T):
     """Multi-token MXFP4 layers with an MXFP4 shared expert: the grouped GEMMs run the shared
     expert as one group of every token (weight 1, SiLU) and the combine adds it, sigmoid-gated,
@@ -440,7 +443,7 @@ def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
-         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4, *WIDE_MX, "tiny-mxfp4-k10"]
+         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4, *WIDE_MX, *WIDE_SH, "tiny-mxfp4-k10"]
 
 
 @pytest.mark.parametrize("name", FUSED)
