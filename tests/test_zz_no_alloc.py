@@ -19,9 +19,14 @@ SPECS = {
     # Q4_K with a shared expert: the grouped Q4_K MFMA path (pair lists, images, shared rows)
     "q4k-shared-grouped": W.LayerSpec(231, 0, W.GGML_Q4_K, 512, 256, 24, 5, W.ROUTE_NORM_TOPK, W.ACT_SILU,
                                       False, False, sh_inter=256),
+    # MXFP4 with an MXFP4 shared expert twice as wide: the grouped path's shared group (its h
+    # images, down rows and sigmoid gates in the scratch)
+    "mxfp4-shared-grouped": W.LayerSpec(232, 0, W.GGML_MXFP4, 512, 384, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                        False, False, sh_inter=768, sh_type=W.GGML_MXFP4),
     "C1-gpt-oss": W.gpt_oss(1, 0),
 }
-TOKENS = {"mxfp4-grouped": (96, 17), "q4k-shared-grouped": (64, 9), "C1-gpt-oss": (200, 33)}
+TOKENS = {"mxfp4-grouped": (96, 17), "q4k-shared-grouped": (64, 9), "mxfp4-shared-grouped": (80, 21),
+          "C1-gpt-oss": (200, 33)}
 # Layers run with MR_OPT_DECODE_KERNEL = MR_DECODE_VALU, which sends both entry points down the
 # VALU path (activations [T, k, I] and shared activations [T, Ish + 1] in the scratch)
 VALU = {"q4k-shared-valu": "q4k-shared-grouped", "mxfp4-valu": "mxfp4-grouped"}
