@@ -129,6 +129,48 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Butterfly steps across lanes l and l ^ 32 (l ^ 16) with gfx950's lane-swap instructions
+// instead of an LDS permute: v_permlane32_swap (v_permlane16_swap) with one register as both
+// operands leaves {v[l], v[l ^ 32]} ({v[l], v[l ^ 16]}) in the two results of lane l, so their
+// sum (maximum) is the step's value, the same bits in both lanes of a pair since the operation
+// is commutative. All 64 lanes active.
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// v + v[l ^ 8] and v + v[l ^ 4] by DPP inside each row of 16 lanes: row_ror:8 reads lane
+// l ^ 8; lanes 0-3 and 8-11 (banks 0, 2) read four lanes up with row_ror:12, lanes 4-7 and
+// 12-15 (banks 1, 3) four down with row_ror:4.
+__device__ __forceinline__ float add_xor8(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float add_xor4(float v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xA, false);
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(lo, __float_as_int(v), 0x12C, 0xF, 0x5, false));
+}
+// wave_sum's butterfly (the pairs l, l ^ o for o = 32 .. 1, so the same bits in every lane and
+// the same bits as wave_sum) without LDS permutes; all 64 lanes active.
+__device__ __forceinline__ float wave_sum_fast(float v) {
+  v = add_xor32(v);
+  v = add_xor16(v);
+  v = add_xor8(v);
+  v = add_xor4(v);
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // l ^ 2
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // l ^ 1
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

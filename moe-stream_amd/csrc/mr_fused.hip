@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
         acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
       }
-      acc = wave_sum(acc);  // the same bits in every lane (butterfly of commutative adds)
+      acc = wave_sum_fast(acc);  // the same bits in every lane (butterfly of commutative adds)
       if (e < a.E) {
         if (a.router_b) acc = acc + rbias;
         if (a.mask) acc = acc + rmask;

@@ -236,8 +236,7 @@ __device__ __forceinline__ float unit_dot(const uint4& hd, const uint4& w0, cons
 
 // The four shares of a row summed: every lane holds its row i's total.
 __device__ __forceinline__ float row_total(float v) {
-  v = v + __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+  return add_xor32(add_xor16(v));
 }
 
 // A wave's units 0..nu-1 (nu >= 1): RING of them are loaded by units_issue (all RING loads are
@@ -376,7 +375,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
           acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
         }
       }
-      acc = wave_sum(acc);  // the same bits in every lane (butterfly of commutative adds)
+      acc = wave_sum_fast(acc);  // the same bits in every lane (butterfly of commutative adds)
       if (e < a.E) {
         if (a.router_b) acc = acc + rbias;
         if (a.mask) acc = acc + rmask;

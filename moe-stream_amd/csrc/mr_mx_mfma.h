@@ -80,8 +80,7 @@ __device__ __forceinline__ void split_block_x2(float a0, float a1, float a2, flo
   for (int t = 0; t < NT; ++t) {
     float m = fmaxf(fmaxf(fmaxf(fabsf(a0), fabsf(a1)), fmaxf(fabsf(a2), fabsf(a3))),
                     fmaxf(fmaxf(fabsf(b0), fabsf(b1)), fmaxf(fabsf(b2), fabsf(b3))));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = max_xor32(max_xor16(m));
     const int ex = (int)((__float_as_uint(m) >> 23) & 0xFFu);  // biased exponent; 0: zero/denormal
     const int sb = ex - 7;                                     // e8m0 byte of 2^(e-7)
     uint32_t c = 0u, d = 0u;
