@@ -51,11 +51,14 @@
 #include "mr_mx_mfma.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mr {
 
 constexpr int kSteps = 23;              // K steps (4 blocks each) per wave: H, I <= 2944
 constexpr int kRouterVec = 12;          // float4 pairs per lane of a router row: H <= 3072
+constexpr int kRouterJ = kRouterVec / 4;  // float4s per lane of one wave's quarter of a router row
+constexpr int kRouterRounds = 4;          // logits per router workgroup at most
 constexpr int kImgVec = 12;             // 16-byte image loads per lane for one slot: I <= 3072
 
 
@@ -85,6 +88,7 @@ struct FusedArgs {
   int act;
   float alpha, limit;
   int R, NG, ND;
+  int rr;  // logits per router workgroup (1, 2 or 4; router_rounds)
   int NS;        // down row groups split into two 8-row workgroups (CU balance; at most four slots)
   int NDR, nsl;  // row groups and slot groups of the down role (ND = NDR * nsl)
   WaitBound wb;  // time limit of the cross-workgroup waits
@@ -329,47 +333,88 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 
   if (bid < a.R) {
     // ------------------------------------------------------------- router
+    // Logits bid * rr .. bid * rr + rr - 1 (experts, then the shared expert's gate row x . w_gi);
+    // wave w takes quarter w of every row's columns, so each wave issues rr * 3 + 3 float4 loads
+    // per lane instead of a whole row and x (a CU's address unit takes 64 bytes a clock: loading
+    // whole rows kept it busy for most of a microsecond), the quarters' sums are added in quarter
+    // order, and wave r finishes logit r.
     __builtin_amdgcn_s_setprio(2);  // the logits gate every other role: router loads issue first
-    const int e = bid * 4 + wave;
-    if (e < a.E + has_sh) {
-      // experts, then the shared expert's gate row (x . w_gi, its sigmoid gate)
-      const float* w = e < a.E ? a.router_w + (size_t)e * a.H : a.sh_gate_inp;
-      // bias and mask are loaded with the rows, not after the reduction (an HBM round trip)
-      const float rbias = (e < a.E && a.router_b) ? a.router_b[e] : 0.f;
-      const float rmask = (e < a.E && a.mask) ? a.mask[e] : 0.f;
-      f32x4 xv[kRouterVec], wv[kRouterVec];  // every load issued before the first use
-      const float* wr = w ? w : a.x;          // no row (no shared gate input): a zero logit
+    const int nlog = a.E + has_sh;
+    auto router = [&](auto nr_c) {
+      constexpr int NR = decltype(nr_c)::value;  // logits of this workgroup
+      const int e0 = bid * NR, ef = e0 + wave;    // ef: the logit this wave finishes (wave < NR)
+      f32x4 xv[kRouterJ], wv[NR][kRouterJ];      // every load issued before the first use
 #pragma unroll
-      for (int j = 0; j < kRouterVec; ++j) {
-        const int c = (lane + 64 * j) * 4;
-        xv[j] = ld4_or0(a.x, c, a.H);
-        wv[j] = ld4_or0(wr, w ? c : a.H, a.H);
-      }
-      if (NORM) {  // x = rms_norm(h)
-        f32x4 nv[kRouterVec];
-        load_lanes4_all(a.nr.w, a.H, nv);
-        const float inv = rms_inv(xv, a.H, a.nr.eps);
+      for (int jj = 0; jj < kRouterJ; ++jj) xv[jj] = ld4_or0(a.x, (lane + 64 * (wave * kRouterJ + jj)) * 4, a.H);
 #pragma unroll
-        for (int j = 0; j < kRouterVec; ++j)
-          xv[j] = f32x4{norm1(xv[j].x, inv, nv[j].x), norm1(xv[j].y, inv, nv[j].y),
-                        norm1(xv[j].z, inv, nv[j].z), norm1(xv[j].w, inv, nv[j].w)};
-      }
-      float acc = 0.f;
+      for (int r = 0; r < NR; ++r) {
+        const int e = e0 + r;
+        // past the last logit (and the shared gate without its input row): x is read instead,
+        // a zero logit that is not published
+        const float* w = e < a.E ? a.router_w + (size_t)e * a.H : (e == a.E && has_sh) ? a.sh_gate_inp : nullptr;
 #pragma unroll
-      for (int j = 0; j < kRouterVec; ++j) {
-        acc = __builtin_fmaf(xv[j].x, wv[j].x, acc);
-        acc = __builtin_fmaf(xv[j].y, wv[j].y, acc);
-        acc = __builtin_fmaf(xv[j].z, wv[j].z, acc);
-        acc = __builtin_fmaf(xv[j].w, wv[j].w, acc);
+        for (int jj = 0; jj < kRouterJ; ++jj) {
+          const int c = (lane + 64 * (wave * kRouterJ + jj)) * 4;
+          wv[r][jj] = ld4_or0(w ? w : a.x, w ? c : a.H, a.H);
+        }
       }
-      acc = wave_sum_fast(acc);  // the same bits in every lane (butterfly of commutative adds)
-      if (e < a.E) {
-        if (a.router_b) acc = acc + rbias;
-        if (a.mask) acc = acc + rmask;
+      // the bias and mask of the logit this wave finishes, loaded with the rows
+      const float rbias = (wave < NR && ef < a.E && a.router_b) ? a.router_b[ef] : 0.f;
+      const float rmask = (wave < NR && ef < a.E && a.mask) ? a.mask[ef] : 0.f;
+      if (NORM) {  // x = rms_norm(h): the quarters' sums of squares, added in quarter order in every wave
+        f32x4 nv[kRouterJ];
+#pragma unroll
+        for (int jj = 0; jj < kRouterJ; ++jj) nv[jj] = ld4_or0(a.nr.w, (lane + 64 * (wave * kRouterJ + jj)) * 4, a.H);
+        float inv;
+        {
+#pragma clang fp contract(off)
+          float ss = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < kRouterJ; ++jj) {
+            ss = ss + xv[jj].x * xv[jj].x;
+            ss = ss + xv[jj].y * xv[jj].y;
+            ss = ss + xv[jj].z * xv[jj].z;
+            ss = ss + xv[jj].w * xv[jj].w;
+          }
+          ss = wave_sum_fast(ss);
+          if (lane == 0) lds_part[wave] = ss;
+          __syncthreads();
+          const float t = ((lds_part[0] + lds_part[1]) + lds_part[2]) + lds_part[3];
+          inv = 1.f / sqrtf(t / (float)a.H + a.nr.eps);
+        }
+#pragma unroll
+        for (int jj = 0; jj < kRouterJ; ++jj)
+          xv[jj] = f32x4{norm1(xv[jj].x, inv, nv[jj].x), norm1(xv[jj].y, inv, nv[jj].y),
+                         norm1(xv[jj].z, inv, nv[jj].z), norm1(xv[jj].w, inv, nv[jj].w)};
       }
-      put_logit(a.fs, (uint32_t)(a.E + has_sh), e, seq, acc);
-      if (a.logits_out && e < a.E && lane == 0) a.logits_out[e] = acc;
-    }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < kRouterJ; ++jj) {
+          acc = __builtin_fmaf(xv[jj].x, wv[r][jj].x, acc);
+          acc = __builtin_fmaf(xv[jj].y, wv[r][jj].y, acc);
+          acc = __builtin_fmaf(xv[jj].z, wv[r][jj].z, acc);
+          acc = __builtin_fmaf(xv[jj].w, wv[r][jj].w, acc);
+        }
+        acc = wave_sum_fast(acc);  // the same bits in every lane
+        if (lane == 0) lds_part[16 + r * 4 + wave] = acc;  // (NORM: words 0-3 are not rewritten)
+      }
+      __syncthreads();
+      if (wave < NR && ef < nlog) {
+        float acc = ((lds_part[16 + wave * 4] + lds_part[16 + wave * 4 + 1]) + lds_part[16 + wave * 4 + 2]) +
+                    lds_part[16 + wave * 4 + 3];
+        if (ef < a.E) {
+          if (a.router_b) acc = acc + rbias;
+          if (a.mask) acc = acc + rmask;
+        }
+        put_logit(a.fs, (uint32_t)nlog, ef, seq, acc);
+        if (a.logits_out && ef < a.E && lane == 0) a.logits_out[ef] = acc;
+      }
+    };
+    if (a.rr == 1) router(std::integral_constant<int, 1>{});
+    else if (a.rr == 2) router(std::integral_constant<int, 2>{});
+    else router(std::integral_constant<int, kRouterRounds>{});
     TRACE(1);
     prefetch_rows(a.pf, bid, a.R, lds_dyn);
     prefetch_norm(a.pf_nw, a.H, bid, lds_dyn);
@@ -665,6 +710,19 @@ uint64_t fused_layer_sync_bytes(const mr_layer& L) { return layer_sync_words(L.E
 static bool fused_multi(const mr_layer& L) { return L.d.top_k + (L.d.sh_gate ? 1u : 0u) > 4u; }
 static bool fused_gen(const mr_layer& L) { return L.d.sh_gate != nullptr || fused_multi(L); }
 
+// Logits per router workgroup: the fewest of 1, 2, 4 with which the routers and the down groups
+// share one dispatch round (plain layers) or the whole grid fits three workgroups per CU.
+static int router_rounds(const mr_layer& L, int n_cu) {
+  const uint64_t has_sh = L.d.sh_gate ? 1u : 0u, n = L.E + has_sh, ktot = L.d.top_k + has_sh;
+  const uint64_t ND = (L.H + 15) / 16 * ((ktot + 3) / 4), NG = L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32);
+  const bool multi = ktot > 4;
+  for (int rr = 1; rr < kRouterRounds; rr *= 2) {
+    const uint64_t R = (n + rr - 1) / rr;
+    if ((multi || R + ND < (uint64_t)n_cu) && R + ND + NG <= 3ull * n_cu && R + ND + NG <= (uint64_t)kMaxGrid) return rr;
+  }
+  return kRouterRounds;
+}
+
 bool fused_supported(const mr_layer& L, int n_cu) {
   if (L.type != MR_GGML_MXFP4 || L.d.top_k > 16) return false;
   const uint64_t has_sh = L.d.sh_gate ? 1u : 0u;
@@ -674,7 +732,8 @@ bool fused_supported(const mr_layer& L, int n_cu) {
     return false;  // a shared expert: MXFP4 like the routed ones, its K steps within a down wave's
   if (L.E + has_sh > (uint64_t)kMaxLogits) return false;
   const uint64_t ktot = L.d.top_k + has_sh, nsl = (ktot + 3) / 4;
-  const uint64_t R = (L.E + has_sh + 3) / 4, ND = (L.H + 15) / 16 * nsl, NG = L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32);
+  const uint64_t ND = (L.H + 15) / 16 * nsl, NG = L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32);
+  const uint64_t R = (L.E + has_sh + router_rounds(L, n_cu) - 1) / router_rounds(L, n_cu);
   if (!fused_multi(L) && R + ND >= (uint64_t)n_cu) return false;  // routers and down groups in one dispatch round
   if (R + ND + NG > 3ull * n_cu) return false;
   if (R + ND + NG > (uint64_t)kMaxGrid) return false;  // the split groups are added only where they fit
@@ -696,13 +755,14 @@ extern "C" void mr_debug_fused_trace(void* dev_buf) { g_fused_trace = (unsigned 
 // down group carry three units; splitting those down groups in halves, the second half
 // in a third-round slot on a CU with two units, caps every CU at 2.5 units.
 struct FusedGrid {
-  int R, ND, NG, NS, NDR, nsl;
+  int R, ND, NG, NS, NDR, nsl, rr;
   int total() const { return R + ND + NG + NS; }
 };
 static FusedGrid fused_grid(const mr_layer& L, int n_cu) {
   FusedGrid g;
   const uint32_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + has_sh;
-  g.R = (int)((L.E + has_sh + 3) / 4);
+  g.rr = router_rounds(L, n_cu);
+  g.R = (int)((L.E + has_sh + g.rr - 1) / g.rr);
   g.NG = (int)(L.d.top_k * (L.I / 32) + has_sh * (L.Ish / 32));
   g.NDR = (int)((L.H + 15) / 16);
   g.nsl = (int)((ktot + 3) / 4);
@@ -797,11 +857,12 @@ hipError_t launch_fused(const Launch& K, const mr_layer& L, const float* x, floa
   a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)k, a.ktot = (int)ktot;
   a.flags = L.d.route_flags, a.act = (int)L.d.act, a.alpha = L.d.alpha, a.limit = L.d.limit;
   const FusedGrid fg = fused_grid(L, n_cu);
-  a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl;
+  a.R = fg.R, a.NG = fg.NG, a.ND = fg.ND, a.NS = fg.NS, a.NDR = fg.NDR, a.nsl = fg.nsl, a.rr = fg.rr;
   a.perm_nc = role_perm_nc(fg.total(), fg.R, fg.NG, n_cu);
   a.dn_delay = dn_delay_rounds(L);
   a.wb = wb;
   a.pf = prefetch_plan(L.next);
+  if (a.pf.w && L.next->type == MR_GGML_MXFP4 && L.next->ctx) a.pf.rpw = router_rounds(*L.next, n_cu);
   a.pf_nw = L.next && L.next->H == L.H ? L.next->norm_w : nullptr;
   a.nr = nr;
   a.lds_img_bytes = (uint32_t)fused_lds_img_bytes(L);

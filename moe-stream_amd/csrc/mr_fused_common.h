@@ -348,17 +348,27 @@ struct PrefetchRows {
   const float* w;   // [E, H] f32, or nullptr: no prefetch
   const float* sh;  // row E (shared-expert gate) or nullptr
   int rows, E, H;
+  int rpw;          // rows per router workgroup of the next layer's MXFP4 kernel, 0: four, one per wave
 };
+// The next layer's router workgroup nb computes rows nb * rpw .. nb * rpw + rpw - 1: with four
+// rows per workgroup (rpw = 0; the Q4_K kernel) one per wave, whole rows; otherwise (the MXFP4
+// kernel: rpw rows, quarter w of every row's columns in wave w) wave w reads quarter w of each.
 __device__ __forceinline__ void prefetch_rows(const PrefetchRows& p, int bid, int R, uint8_t* lds) {
   if (!p.w) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int nb = bid; nb * 4 < p.rows; nb += R) {
-    const int e = nb * 4 + wave;
-    if (e < p.rows) {
-      const float* src = e < p.E ? p.w + (size_t)e * p.H : p.sh;
-      for (int j = 0; j * 256 < p.H; ++j) {  // 64 lanes x 16 bytes per load
-        const int c = min(j * 256 + lane * 4, p.H - 4);
-        __builtin_amdgcn_global_load_lds(src + c, lds + wave * 1024, 16, 0, 0);
+  const int rpw = p.rpw ? p.rpw : 4;
+  const int nj = (p.H + 255) / 256;                   // 64 lanes x 16 bytes per load
+  const int jq = p.rpw ? (nj + 3) / 4 : nj;           // loads per row and wave
+  const int j0 = p.rpw ? wave * jq : 0, j1 = min(nj, j0 + jq);
+  for (int nb = bid; nb * rpw < p.rows; nb += R) {
+    for (int r = p.rpw ? 0 : wave; r < rpw; r += p.rpw ? 1 : 4) {
+      const int e = nb * rpw + r;
+      if (e < p.rows) {
+        const float* src = e < p.E ? p.w + (size_t)e * p.H : p.sh;
+        for (int j = j0; j < j1; ++j) {
+          const int c = min(j * 256 + lane * 4, p.H - 4);
+          __builtin_amdgcn_global_load_lds(src + c, lds + wave * 1024, 16, 0, 0);
+        }
       }
     }
   }
@@ -378,7 +388,7 @@ __device__ __forceinline__ void prefetch_norm(const float* nw, int H, int bid, u
 }
 // Host side: the plan for the hint set with mr_layer_set_next (no prefetch without one).
 inline PrefetchRows prefetch_plan(const mr_layer* n) {
-  PrefetchRows p{nullptr, nullptr, 0, 0, 0};
+  PrefetchRows p{nullptr, nullptr, 0, 0, 0, 0};
   if (!n || !n->d.router_w || n->H < 4) return p;
   p.w = n->d.router_w;
   p.sh = n->d.sh_gate ? n->d.sh_gate_inp : nullptr;
