@@ -326,7 +326,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   const int bid = role_index((int)blockIdx.x, a.perm_nc, a.R, a.ND, a.NG);  // role index
   const int nbH = a.H >> 5, nbI = a.I >> 5;
   TRACE(0);
-  const uint32_t seq = ld_sc1(wg_seq_word(a.fs));
+  // This launch's number (wg_seq_word). Its load goes to the device-coherent level, a memory
+  // round trip: each role issues it after its own first loads, so that it is in flight with
+  // them instead of ahead of them (loaded first, it was waited for before any other load issued).
+  uint32_t seq;
   const int has_sh = GEN ? a.has_sh : 0, ktot = GEN ? a.ktot : a.k;
   const RouteCfg rc{a.fs, (uint32_t)(a.E + has_sh), a.E, a.k, a.flags, a.wb, a.trace};
   if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
@@ -361,6 +364,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       // the bias and mask of the logit this wave finishes, loaded with the rows
       const float rbias = (wave < NR && ef < a.E && a.router_b) ? a.router_b[ef] : 0.f;
       const float rmask = (wave < NR && ef < a.E && a.mask) ? a.mask[ef] : 0.f;
+      seq = ld_sc1(wg_seq_word(a.fs));
       if (NORM) {  // x = rms_norm(h): the quarters' sums of squares, added in quarter order in every wave
         f32x4 nv[kRouterJ];
 #pragma unroll
@@ -435,9 +439,17 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       for (int j = 0; j < kRounds; ++j) {
         const int b = (tid >> 3) + 32 * j;
         const float* xb = a.x + b * 32 + 2 * m;
-        lo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb) : f32x2{0.f, 0.f};        // 2m, 2m+1
-        hi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb + 16) : f32x2{0.f, 0.f};   // 2m+16, 2m+17
+        if constexpr (NORM) {  // every load issued at once (a clamped block, zero selected after)
+          const float* xc = a.x + min(b, nbH - 1) * 32 + 2 * m;
+          const f32x2 l0 = *reinterpret_cast<const f32x2*>(xc), h0 = *reinterpret_cast<const f32x2*>(xc + 16);
+          lo[j] = b < nbH ? l0 : f32x2{0.f, 0.f};
+          hi[j] = b < nbH ? h0 : f32x2{0.f, 0.f};
+        } else {  // conditional: fewer requests beside the router's loads (measured faster here)
+          lo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb) : f32x2{0.f, 0.f};       // 2m, 2m+1
+          hi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(xb + 16) : f32x2{0.f, 0.f};  // 2m+16, 2m+17
+        }
       }
+      if (!NORM) seq = ld_sc1(wg_seq_word(a.fs));
       if (NORM) {  // x = rms_norm(h): each wave derives inv the way the router waves do
         f32x4 hv[kRouterVec];
         load_lanes4_all(a.x, a.H, hv);
@@ -449,6 +461,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           nlo[j] = b < nbH ? *reinterpret_cast<const f32x2*>(wb) : f32x2{0.f, 0.f};
           nhi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(wb + 16) : f32x2{0.f, 0.f};
         }
+        seq = ld_sc1(wg_seq_word(a.fs));
         const float inv = rms_inv(hv, a.H, a.nr.eps);
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
@@ -551,6 +564,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     if (tid == 0) count<64>(a.fs + FS_GU, gid);
   } else {
     // ------------------------------------------------------------- down
+    seq = ld_sc1(wg_seq_word(a.fs));  // needed at once: the routing poll compares its flags
     // Row group q of 16 output rows. The first NS groups are split: rows 0-7 here, rows
     // 8-15 in a workgroup after the gate/up range (half 2). A half's idle lanes read the
     // row of their partner lane (i ^ 8): the same addresses, so no extra HBM bytes.
