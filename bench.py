@@ -339,7 +339,16 @@ def trace_decode(a) -> None:
     li = 5 % len(specs)
     s0 = specs[li]
     if s0.mxfp4:
-        R, ND, NG = (s0.n_experts + 3) // 4, (s0.hidden + 15) // 16, s0.top_k * (s0.inter // 32)
+        # the MXFP4 kernel's router workgroups take rr = 1, 2 or 4 logits each (router_rounds):
+        # the fewest that keep routers and down groups in one dispatch round (or, with more than
+        # four slots, the grid within three workgroups per CU)
+        has_sh = 1 if s0.sh_inter else 0
+        ktot = s0.top_k + has_sh
+        ND, NG = (s0.hidden + 15) // 16 * ((ktot + 3) // 4), s0.top_k * (s0.inter // 32) + has_sh * (s0.sh_inter // 32)
+        n_cu = 256
+        rr = next((r for r in (1, 2) if (ktot > 4 or -(-(s0.n_experts + has_sh) // r) + ND < n_cu)
+                   and -(-(s0.n_experts + has_sh) // r) + ND + NG <= 3 * n_cu), 4)
+        R = -(-(s0.n_experts + has_sh) // rr)
     else:  # Q4_K: the shared expert is one more router row and one more gate/up slot
         has_sh = 1 if s0.sh_inter else 0
         R, ND, NG = (s0.n_experts + has_sh + 3) // 4, s0.hidden // 16, (s0.top_k + has_sh) * (s0.inter // 16)
