@@ -69,6 +69,8 @@ def parse():
     ap.add_argument("--probe", action="store_true",
                     help="only measure the ceilings: a graph of empty kernels (the kernel-boundary floor) and "
                          "plain streaming reads of the decode layers' byte counts")
+    ap.add_argument("--probe-flags", action="store_true",
+                    help="only measure flag round trips between two workgroups (within one XCD and across XCDs)")
     ap.add_argument("--probe-eager", action="store_true",
                     help="the plain reads of --probe launched one at a time (512 workgroups, 8 loads in flight), "
                          "for a kernel trace (rocprofv3 --kernel-trace) of their device durations")
@@ -256,6 +258,36 @@ def probes() -> None:
     pool.free(), sink.free()
     ctx.close()
     print(json.dumps(out), flush=True)
+
+
+def probe_flags() -> None:
+    """Round trips of an agent-coherent flag between two workgroups of one launch, the hand-off
+    the fused decode kernels use (a stores i, b polls for it and stores i back, a polls for
+    that; 2,000 round trips per run, 5 runs per pair). Workgroup b runs on XCD b mod 8: pairs
+    (0, 8) and (3, 67) share an XCD, (0, 1) and (0, 4) do not. Device-clock time per round trip,
+    with both workgroups' XCC_ID and HW_ID."""
+    import moe_rocm as M
+
+    ctx = M.Context(0)
+    words, res = ctx.alloc(64 * 4), ctx.alloc(4 * 8)
+    n = 2000
+    out = {"probe": "flag round trips", "round_trips_per_run": n, "pairs": []}
+    for a_, b_ in ((0, 8), (3, 67), (0, 1), (0, 4), (0, 255)):
+        runs, ids = [], None
+        for _ in range(5):
+            ctx.probe_flags(words, a_, b_, n, res)
+            ctx.sync()
+            r = res.download(np.uint64).astype(np.int64)
+            if int(r[1]) != n:
+                sys.exit(f"probe_flags: pair {a_},{b_} completed {int(r[1])} of {n} round trips")
+            runs.append(float(r[0]) / 100.0 / n)  # 100 MHz clock -> us per round trip
+            ids = [{"xcc": int(v) >> 32, "hw_id": hex(int(v) & 0xFFFFFFFF)} for v in (r[2], r[3])]
+        out["pairs"].append({"workgroups": [a_, b_], "same_xcd": ids[0]["xcc"] == ids[1]["xcc"], "ids": ids,
+                             "us_per_round_trip": {"median": round(float(np.median(runs)), 3),
+                                                   "min": round(min(runs), 3), "max": round(max(runs), 3)}})
+    print(json.dumps(out), flush=True)
+    words.free(), res.free()
+    ctx.close()
 
 
 def probes_eager() -> None:
@@ -689,6 +721,9 @@ def main():
         return
     if a.probe:
         probes()
+        return
+    if a.probe_flags:
+        probe_flags()
         return
     if a.probe_eager:
         probes_eager()

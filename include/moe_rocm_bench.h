@@ -46,6 +46,15 @@ int mr_probe_empty(mr_ctx* ctx, uint32_t n_workgroups);
 int mr_probe_touch(mr_ctx* ctx, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink);
 int mr_probe_tiles(mr_ctx* ctx, const void* src, uint32_t row_bytes, uint32_t n_tiles, uint32_t n_workgroups,
                    uint32_t depth, uint32_t* sink);
+/* Flag round trips between workgroups wg_a and wg_b of one launch (wg_a != wg_b, both < 1024;
+ * workgroup b runs on XCD b mod 8) through the device-coherent level, as the fused decode
+ * kernels hand data between workgroups: a stores i, b polls for it and stores i back, a polls
+ * for that, i = 1 .. n_round_trips (<= 100000). words: 64 device u32, cleared by the call;
+ * result: 4 device u64 = device-clock ticks (100 MHz) of wg_a over the round trips, round trips
+ * completed (a poll gives up after 100 ms), and the XCC_ID << 32 | HW_ID of wg_a and wg_b.
+ * Profile name "probe_flags". */
+int mr_probe_flags(mr_ctx* ctx, uint32_t* words, uint32_t wg_a, uint32_t wg_b, uint32_t n_round_trips,
+                   unsigned long long* result);
 
 #ifdef __cplusplus
 }

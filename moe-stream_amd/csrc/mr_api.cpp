@@ -933,6 +933,20 @@ int mr_probe_touch(mr_ctx* c, const void* src, uint64_t nbytes, uint32_t stride,
   return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_touch launch");
 }
 
+int mr_probe_flags(mr_ctx* c, uint32_t* words, uint32_t wg_a, uint32_t wg_b, uint32_t n_round_trips,
+                   unsigned long long* result) {
+  if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
+  if (!words || !result) return set_err(c, MR_E_INVAL, "probe_flags: NULL words or result");
+  if (wg_a == wg_b || wg_a > 1023 || wg_b > 1023 || n_round_trips == 0 || n_round_trips > 100000)
+    return set_err(c, MR_E_INVAL, "probe_flags: workgroups %u, %u and %u round trips out of range", wg_a, wg_b,
+                   n_round_trips);
+  if (!has_dev(c)) return set_err(c, MR_E_NODEV, "host-only context");
+  int rc = bind(c);
+  if (rc) return rc;
+  const hipError_t e = mr::launch_probe_flags(c->launch(), words, (int)wg_a, (int)wg_b, (int)n_round_trips, result);
+  return e == hipSuccess ? MR_OK : hip_fail(c, e, "probe_flags launch");
+}
+
 int mr_probe_empty(mr_ctx* c, uint32_t n_wg) {
   if (!c) return set_err(nullptr, MR_E_INVAL, "context is NULL");
   if (n_wg == 0) return set_err(c, MR_E_INVAL, "probe_empty: n_workgroups is 0");

@@ -187,6 +187,7 @@ hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uin
                               uint32_t depth, uint32_t* sink);
 hipError_t launch_probe_touch(const Launch& K, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink);
 hipError_t launch_probe_empty(const Launch& K, uint32_t n_wg);
+hipError_t launch_probe_flags(const Launch& K, uint32_t* words, int a, int b, int n, unsigned long long* res);
 // With `device` current: this device's address of the static scratch array (looked up once
 // per device).
 hipError_t static_scratch_init(int device, void** out);

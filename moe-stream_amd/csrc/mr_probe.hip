@@ -5,6 +5,8 @@
 #include "mr_device.h"
 #include "mr_internal.h"
 
+#include <algorithm>
+
 namespace mr {
 
 // Workgroup b reads its own contiguous range of the buffer (per16 pieces of 16 bytes), thread
@@ -187,6 +189,55 @@ hipError_t launch_probe_tiles(const Launch& K, const void* src, uint32_t rb, uin
 hipError_t launch_probe_touch(const Launch& K, const void* src, uint64_t nbytes, uint32_t stride, uint32_t* sink) {
   ProfScope ps(K, "probe_touch");
   hipLaunchKernelGGL(k_probe_touch, dim3(256), dim3(256), 0, K.s, static_cast<const uint8_t*>(src), nbytes, stride, sink);
+  return hipGetLastError();
+}
+
+// Flag round trips between two workgroups, a and b, through the device-coherent level, the
+// hand-off the fused decode kernels use (agent-scope stores and polling loads). Thread 0 of a
+// stores i to word 0 and polls word 32 (another 128-byte line) until it reads i; thread 0 of b
+// polls word 0 for i and stores i to word 32; i = 1 .. n. Workgroups are dealt to the XCDs in
+// turn (b mod 8), so b - a = 8 keeps both on one XCD and an odd difference puts them on two.
+// Every poll gives up once the device clock has run limit ticks (100 MHz) past the start of the
+// wait, so both threads end whatever happens. res: [0] clock ticks a spent on the n round trips,
+// [1] round trips completed, [2] a's XCC_ID << 32 | HW_ID, [3] the same of b. The words are zero
+// when the kernel starts (the host clears them).
+__global__ __launch_bounds__(64) void k_probe_flags(uint32_t* w, int a, int b, int n, uint64_t limit,
+                                                    unsigned long long* res) {
+  if (threadIdx.x != 0 || ((int)blockIdx.x != a && (int)blockIdx.x != b)) return;
+  const bool is_a = (int)blockIdx.x == a;
+  uint32_t* mine = w + (is_a ? 0 : 32);
+  const uint32_t* theirs = w + (is_a ? 32 : 0);
+  const unsigned long long id = ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |
+                                (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  int done = 0;
+  for (int i = 1; i <= n; ++i) {
+    if (is_a) __hip_atomic_store(mine, (uint32_t)i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long w0 = __builtin_amdgcn_s_memrealtime();
+    bool seen = false;
+    while (!(seen = __hip_atomic_load(theirs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)i) &&
+           __builtin_amdgcn_s_memrealtime() - w0 < limit) {
+    }
+    if (!seen) break;
+    if (!is_a) __hip_atomic_store(mine, (uint32_t)i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    done = i;
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (is_a) {
+    res[0] = t1 - t0;
+    res[1] = (unsigned long long)done;
+    res[2] = id;
+  } else {
+    res[3] = id;
+  }
+}
+
+hipError_t launch_probe_flags(const Launch& K, uint32_t* words, int a, int b, int n, unsigned long long* res) {
+  ProfScope ps(K, "probe_flags");
+  const hipError_t e = hipMemsetAsync(words, 0, 64 * sizeof(uint32_t), K.s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_probe_flags, dim3((unsigned)(std::max(a, b) + 1)), dim3(64), 0, K.s, words, a, b, n,
+                     (uint64_t)10000000 /* 100 ms */, res);
   return hipGetLastError();
 }
 

@@ -95,6 +95,7 @@ _SIGS = {
     "mr_moe_forward_batched_residual": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _f32, _vp]),
     "mr_probe_read": (C.c_int, [_vp, _vp, _u64, _u32, _u32, _vp]),
     "mr_probe_empty": (C.c_int, [_vp, _u32]),
+    "mr_probe_flags": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
     "mr_probe_tiles": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "mr_probe_touch": (C.c_int, [_vp, _vp, _u64, _u32, _vp]),
     "mr_moe_forward_batched_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp]),
@@ -238,6 +239,9 @@ class Context:
 
     def probe_empty(self, n_workgroups: int) -> None:
         self.check(_lib.mr_probe_empty(self.h, n_workgroups))
+
+    def probe_flags(self, words, wg_a: int, wg_b: int, n_round_trips: int, result) -> None:
+        self.check(_lib.mr_probe_flags(self.h, _ptr(words), wg_a, wg_b, n_round_trips, _ptr(result)))
 
     def synth_blocks(self, ggml_type: int, dst: "DeviceBuffer", n_blocks: int, seed: int,
                      offset: int = 0) -> None:

@@ -24,7 +24,8 @@ def declared_functions(headers=(HEADER, BENCH_HEADER)):
 
 def test_bench_support_stays_out_of_the_drop_in_header():
     core = declared_functions((HEADER,))
-    for n in ("mr_synth_blocks", "mr_probe_read", "mr_probe_empty", "mr_probe_tiles", "mr_probe_touch"):
+    for n in ("mr_synth_blocks", "mr_probe_read", "mr_probe_empty", "mr_probe_tiles", "mr_probe_touch",
+              "mr_probe_flags"):
         assert n not in core and n in declared_functions((BENCH_HEADER,))
 
 
