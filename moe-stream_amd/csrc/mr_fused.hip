@@ -319,6 +319,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   __shared__ uint32_t sel_k[16];
   __shared__ uint32_t route_tmp[128];  // routing: compacted candidates
   __shared__ int ok_flag;
+  __shared__ float lds_xw[2];  // gate/up: the shared gate logit and (NORM) the norm scale, as polled
   __shared__ __align__(16) uint8_t lds_zero[32];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -331,7 +332,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
   // them instead of ahead of them (loaded first, it was waited for before any other load issued).
   uint32_t seq;
   const int has_sh = GEN ? a.has_sh : 0, ktot = GEN ? a.ktot : a.k;
-  const RouteCfg rc{a.fs, (uint32_t)(a.E + has_sh), a.E, a.k, a.flags, a.wb, a.trace};
+  // Published words: the E logits, the shared expert's gate logit, and with the fused norm its
+  // scale 1/sqrt(mean(h^2) + eps), which the gate/up role applies to its dot products instead of
+  // reducing the sum of squares itself.
+  const uint32_t nlw = (uint32_t)(a.E + has_sh + (NORM ? 1 : 0));
+  const RouteCfg rc{a.fs, nlw, a.E, a.k, a.flags, a.wb, a.trace};
   if (tid < 8) reinterpret_cast<uint32_t*>(lds_zero)[tid] = 0u;  // read after later barriers
 
   if (bid < a.R) {
@@ -365,11 +370,11 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
       const float rbias = (wave < NR && ef < a.E && a.router_b) ? a.router_b[ef] : 0.f;
       const float rmask = (wave < NR && ef < a.E && a.mask) ? a.mask[ef] : 0.f;
       seq = ld_sc1(wg_seq_word(a.fs));
+      float inv = 1.f;
       if (NORM) {  // x = rms_norm(h): the quarters' sums of squares, added in quarter order in every wave
         f32x4 nv[kRouterJ];
 #pragma unroll
         for (int jj = 0; jj < kRouterJ; ++jj) nv[jj] = ld4_or0(a.nr.w, (lane + 64 * (wave * kRouterJ + jj)) * 4, a.H);
-        float inv;
         {
 #pragma clang fp contract(off)
           float ss = 0.f;
@@ -412,9 +417,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           if (a.router_b) acc = acc + rbias;
           if (a.mask) acc = acc + rmask;
         }
-        put_logit(a.fs, (uint32_t)nlog, ef, seq, acc);
+        put_logit(a.fs, nlw, ef, seq, acc);
         if (a.logits_out && ef < a.E && lane == 0) a.logits_out[ef] = acc;
       }
+      if (NORM && bid == 0 && wave == 0) put_logit(a.fs, nlw, nlog, seq, inv);  // the norm scale
     };
     if (a.rr == 1) router(std::integral_constant<int, 1>{});
     else if (a.rr == 2) router(std::integral_constant<int, 2>{});
@@ -450,9 +456,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
         }
       }
       if (!NORM) seq = ld_sc1(wg_seq_word(a.fs));
-      if (NORM) {  // x = rms_norm(h): each wave derives inv the way the router waves do
-        f32x4 hv[kRouterVec];
-        load_lanes4_all(a.x, a.H, hv);
+      if (NORM) {  // the image of h * norm_w; the scale 1/rms(h), published by the router, is
+                   // applied to the dot products (they are linear in x)
         f32x2 nlo[kRounds], nhi[kRounds];
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
@@ -462,11 +467,10 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           nhi[j] = b < nbH ? *reinterpret_cast<const f32x2*>(wb + 16) : f32x2{0.f, 0.f};
         }
         seq = ld_sc1(wg_seq_word(a.fs));
-        const float inv = rms_inv(hv, a.H, a.nr.eps);
 #pragma unroll
         for (int j = 0; j < kRounds; ++j) {
-          lo[j] = f32x2{norm1(lo[j].x, inv, nlo[j].x), norm1(lo[j].y, inv, nlo[j].y)};
-          hi[j] = f32x2{norm1(hi[j].x, inv, nhi[j].x), norm1(hi[j].y, inv, nhi[j].y)};
+          lo[j] = f32x2{lo[j].x * nlo[j].x, lo[j].y * nlo[j].y};
+          hi[j] = f32x2{hi[j].x * nhi[j].x, hi[j].y * nhi[j].y};
         }
       }
 #pragma unroll
@@ -490,9 +494,13 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
     RouteState rs;
     const int rw = (int)(blockIdx.x >> 8) & 3;
     if (wave == rw) {
-      const bool routed = route_select<MR_ROUTE_SLEEP, QWEN>(rc, seq, sel_i, sel_k, route_tmp, rs);
+      const bool routed = route_select<MR_ROUTE_SLEEP, QWEN, GEN || NORM>(rc, seq, sel_i, sel_k, route_tmp, rs);
       if (lane == 0) ok_flag = routed ? 1 : 0;
       if (!routed && lane == 0) fail(a.err);
+      // the polled extra words: lane 0 the shared gate logit (with a shared expert), the next
+      // lane the norm scale (NORM)
+      if (GEN && has_sh && lane == 0) lds_xw[0] = rs.xv;
+      if (NORM && lane == has_sh) lds_xw[1] = rs.xv;
     }
     XTRACE(wave);  // per wave: at the routing barrier
     __syncthreads();  // selection and x image ready
@@ -511,9 +519,12 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
                          (uint64_t)(pair * 32 + tile * 16) * rb;
       // the epilogue's biases (wave 0, lanes < 32) and shared gate logit, loaded before the stream
       float gbias = 0.f, ubias = 0.f;
-      // every lane, no condition (a load under a lane condition is waited for at once): the
-      // shared gate logit, or the first logit when there is no shared expert (unused then)
-      const float zsh = get_logit(a.fs, (uint32_t)(a.E + has_sh), has_sh ? a.E : 0);
+      // A logit word reloaded here (agent-coherent, unused without a shared expert) holds back the
+      // stream's first wait by a round trip; without it the plain kernel measured 0.15 us slower
+      // per launch (the streams then start into the routers' next-layer prefetch and the down
+      // workgroups' polls). The shared gate logit itself comes from the routing wave's poll.
+      constexpr bool kHold = !NORM;  // with the fused norm the same load made no difference
+      const float zhold = kHold ? get_logit(a.fs, nlw, 0) : 0.f;
       if (wave == 0 && lane < 32 && !sh) {
         const size_t bi = (size_t)e * a.I + pair * 32 + lane;
         if (a.gate_b) gbias = a.gate_b[bi];
@@ -526,7 +537,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
                                   });
       XTRACE(4 + wave);  // per wave: chain done
       TRACE(3);
-      if (wave == 0 && has_sh && lane == 0) sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(zsh) : 1.f;
+      if (wave == 0 && has_sh && lane == 0) sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(lds_xw[0] + zhold * 0.f) : 1.f;
       // column sum over the kTerms columns (= quad 0 of each 16-lane row)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -539,6 +550,7 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
           const int t2 = lane >> 4, r16 = lane & 15;
           float gv = lds_part[(0 * 2 + t2) * 16 + r16];
           float uv = lds_part[(1 * 2 + t2) * 16 + r16];
+          if (NORM) gv = gv * lds_xw[1], uv = uv * lds_xw[1];  // x = (h * norm_w) / rms(h)
           if (!sh && a.gate_b) gv = gv + gbias;
           if (!sh && a.up_b) uv = uv + ubias;
           const float h = (!sh && a.act == MR_ACT_SWIGLU_OAI) ? swiglu_oai(gv, uv, a.alpha, a.limit) : silu_mul(gv, uv);
@@ -716,7 +728,8 @@ __global__ __launch_bounds__(256, 3) void k_fused_mxfp4(FusedArgs a) {
 }
 
 // Shapes the fused kernel runs; others take the VALU path.
-uint64_t fused_layer_sync_bytes(const mr_layer& L) { return layer_sync_words(L.E + (L.d.sh_gate ? 1u : 0u)) * 4; }
+// Room for the logits, the shared gate logit and the fused norm's scale.
+uint64_t fused_layer_sync_bytes(const mr_layer& L) { return layer_sync_words(L.E + (L.d.sh_gate ? 1u : 0u) + 1u) * 4; }
 
 // More than four slots (top_k > 4, or a shared expert with top_k = 4): one down workgroup
 // per row group and group of four slots. A shared expert or more than four slots: the GEN

@@ -614,6 +614,7 @@ struct RouteState {
   float v[kRouteVals];  // this lane's logits
   uint32_t my_key;
   int my_e;
+  float xv;  // the extra entry E + lane (lane < n_logits - E) as polled, else 0
 };
 // The selection by key (topk_slots for one or two key columns, else topk_slots_wide) into
 // sel_i/sel_k; returns the k-th largest key. CHECK: need = prob_exact_needed on the live
@@ -688,14 +689,16 @@ __device__ __forceinline__ void prob_select(const uint32_t (&pkey)[kRouteVals], 
 // extra entry re-read entry 0): a load under a per-lane condition sits in its own branch, and
 // the wait for it at the join would make the loads one round trip each. True when every
 // entry carries this launch's flag; v gets the logits (-inf past E).
-template <int NJ>
-__device__ __forceinline__ bool poll_logits(const uint64_t* lw, int E, int ex, uint32_t flag, float (&v)[kRouteVals]) {
+template <int NJ, bool XTRA>
+__device__ __forceinline__ bool poll_logits(const uint64_t* lw, int E, int ex, uint32_t flag, float (&v)[kRouteVals],
+                                            float& xv) {
   const int lane = threadIdx.x & 63;
   uint64_t w[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) w[j] = ld64_sc1(lw + min(lane + 64 * j, E - 1));
   const uint64_t wx = ld64_sc1(lw + (ex >= 0 ? ex : 0));
   uint32_t bad = (ex >= 0 && (uint32_t)(wx >> 32) != flag) ? 1u : 0u;
+  if (XTRA) xv = ex >= 0 ? __uint_as_float((uint32_t)wx) : 0.f;
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) {
     const bool in = j < NJ && lane + 64 * j < E;
@@ -707,7 +710,8 @@ __device__ __forceinline__ bool poll_logits(const uint64_t* lw, int E, int ex, u
 
 // QWEN: compile in the near-tie check (layers whose flags lack MR_ROUTE_SOFTMAX_AFTER_TOPK rank
 // probabilities); a kernel instantiated without it ranks by logit alone.
-template <int SLEEP = MR_ROUTE_SLEEP, bool QWEN = true>
+// XTRA: keep the polled extra entries (RouteState::xv).
+template <int SLEEP = MR_ROUTE_SLEEP, bool QWEN = true, bool XTRA = false>
 __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i, uint32_t* sel_k, uint32_t* tmp,
                                    RouteState& st) {
   const int lane = threadIdx.x & 63;
@@ -721,14 +725,14 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   const uint64_t* lw = logit_copy(rc.fs, rc.n_logits, (int)(blockIdx.x % kLogitCopies));
   const uint32_t flag = seq + 1u;
   const int ex = lane < (int)rc.n_logits - rc.E ? rc.E + lane : -1;  // an extra entry of this lane
-  float v[kRouteVals];
+  float v[kRouteVals], xv = 0.f;
   WaitTimer tm;
   for (uint32_t it = 0;; ++it) {
     // nj is wave-uniform: one straight-line poll per column count (6 and 7 read 8 columns)
-    const bool ok = nj <= 1   ? poll_logits<1>(lw, rc.E, ex, flag, v)
-                    : nj <= 2 ? poll_logits<2>(lw, rc.E, ex, flag, v)
-                    : nj <= 4 ? poll_logits<4>(lw, rc.E, ex, flag, v)
-                              : poll_logits<8>(lw, rc.E, ex, flag, v);
+    const bool ok = nj <= 1   ? poll_logits<1, XTRA>(lw, rc.E, ex, flag, v, xv)
+                    : nj <= 2 ? poll_logits<2, XTRA>(lw, rc.E, ex, flag, v, xv)
+                    : nj <= 4 ? poll_logits<4, XTRA>(lw, rc.E, ex, flag, v, xv)
+                              : poll_logits<8, XTRA>(lw, rc.E, ex, flag, v, xv);
     if (ok) {
 #ifdef MR_FUSED_TRACE
       if (rc.trace && threadIdx.x == 0) rc.trace[blockIdx.x * 32 + 10] = it;  // polls before the logits were seen
@@ -758,6 +762,7 @@ __device__ inline bool route_select(const RouteCfg& rc, uint32_t seq, int* sel_i
   RTRACE(5);
 #pragma unroll
   for (int j = 0; j < kRouteVals; ++j) st.v[j] = v[j];
+  st.xv = xv;
   st.my_key = lane < rc.k ? sel_k[lane] : 0u;
   st.my_e = lane < rc.k ? sel_i[lane] : 0;
   RTRACE(7);
