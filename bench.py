@@ -12,9 +12,9 @@ resident in HBM). `roofline` is the dominant kernel's algorithmic bytes per
 launch over its average launch duration, measured with HIP events on the
 library's stream. `cpu_baseline` times the CPU oracle (the C restatement of the
 reference's CPU path) on a bounded sample on this host. `extra_configs` (default run
-only) holds the same measurement, with fewer steps and no CPU leg, for C1, C3 and C4
-(decode) and C5 (batched): value, unit, dominant kernel, its average launch and its
-roofline fraction.
+only) holds the same measurement, with fewer steps and no CPU leg, for C1, C2 chained through the
+fused norm and residual, C3 and C4 (decode) and C5 (batched): value, unit, dominant kernel, its
+average launch and its roofline fraction.
 """
 from __future__ import annotations
 
@@ -54,7 +54,7 @@ def parse():
                     help="do not link each layer to the next (mr_layer_set_next)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true",
-                    help="headline only: skip the C1, C3, C4 and C5 rows of extra_configs")
+                    help="headline only: skip the C1, C2-chained, C3, C4 and C5 rows of extra_configs")
     ap.add_argument("--profile-tokens", type=int, default=16)
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle threads for the CPU baseline (0: every logical core, as the reference's available_parallelism)")
@@ -765,29 +765,43 @@ def main():
 # The other configurations, measured after the headline in the default run: decode tokens
 # through every layer of C1 (8 independent layer copies), C3 and C4, and the C5 batched step,
 # each with fewer timed steps and no CPU leg, so the whole default run stays within minutes.
-EXTRA_STEPS = {1: 512, 3: 256, 4: 256, 5: 20}
+# "2c": C2 with the hidden state carried through the layers by mr_moe_forward_residual (fused
+# post-attention norm and residual add), the path a model's decode takes
+EXTRA_STEPS = {1: 512, "2c": 256, 3: 256, 4: 256, 5: 20}
 
 
 def extra_configs(a, ctx, M, W, kernel_opt) -> list:
+    import copy
+
     rows = []
-    for cfg, K in EXTRA_STEPS.items():
+    for key, K in EXTRA_STEPS.items():
         t0 = time.perf_counter()
+        cfg = 2 if key == "2c" else key
         if cfg == 5:
             o = bench_batched(a, ctx, M, W, W.config_layers(5)[0], 5, W.CONFIG_TOKENS[5], K, 3, False)
             ok = True
         else:
-            o, ok = bench_decode(a, ctx, M, W, cfg, K, 4, kernel_opt, False, 4)
+            ac = a
+            if key == "2c":
+                ac = copy.copy(a)
+                ac.decode = "chain"
+            o, ok = bench_decode(ac, ctx, M, W, cfg, K, 4, kernel_opt, False, 4)
         r = o["roofline"] or {}
-        rows.append({"config_id": cfg, "workload": o["config"]["workload"], "metric": o["metric"],
+        workload = o["config"]["workload"]
+        if key == "2c":
+            workload += "; fused post-attention RMSNorm + residual, hidden state carried through the layers"
+        rows.append({"config_id": cfg, "workload": workload, "metric": o["metric"],
                      "value": o["value"], "unit": o["unit"], "steps": o["steps"], "ms_per_step": o["ms_per_step"],
                      "dtype": o["dtype"], "kernel": r.get("kernel"), "avg_launch_us": r.get("avg_launch_us"),
                      "roofline_bound": r.get("bound"), "achieved": r.get("achieved"), "peak": r.get("peak"),
                      "roofline_unit": r.get("unit"), "frac": r.get("frac"), "hbm_frac": o.get("hbm_frac"),
                      "output_check_pass": o["output_check"]["pass"] if "output_check" in o else None,
                      "seconds": round(time.perf_counter() - t0, 1)})
-        log(f"extra C{cfg}: {o['value']} {o['unit']}, frac {r.get('frac')}, {rows[-1]['seconds']} s")
+        if key == "2c":
+            rows[-1]["decode"] = "chain"
+        log(f"extra C{key}: {o['value']} {o['unit']}, frac {r.get('frac')}, {rows[-1]['seconds']} s")
         if not ok:
-            log(f"output check FAILED on C{cfg}")
+            log(f"output check FAILED on C{key}")
             sys.exit(1)
     return rows
 
