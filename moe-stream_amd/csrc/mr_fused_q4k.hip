@@ -98,6 +98,7 @@ struct Q4Args {
   PrefetchRows pf;  // the next layer's router rows (router workgroups read them)
   NormResid nr;     // fused RMSNorm of x and residual added to y (off: nr.w == nullptr)
   unsigned long long* trace;
+  int nsh;  // slots of the shared expert: Ish / I (slot k + j: its rows and columns j*I .. j*I + I - 1)
 };
 
 // ---- int8 two-term split ------------------------------------------------------------------
@@ -141,11 +142,17 @@ __device__ __forceinline__ UnitLane unit_lane(uint32_t rb) {
   return u;
 }
 
-__device__ __forceinline__ void unit_load(const uint8_t* p, const UnitLane& ul, uint4& hd, uint4& w0, uint4& w1) {
-  hd = *reinterpret_cast<const uint4*>(p + ul.o_hd);
-  w0 = *reinterpret_cast<const uint4*>(p + ul.o_w0);
-  w1 = *reinterpret_cast<const uint4*>(p + ul.o_w1);
+// d: extra byte offset of the lane's row (rows of another stride than the UnitLane's)
+__device__ __forceinline__ void unit_load(const uint8_t* p, const UnitLane& ul, uint4& hd, uint4& w0, uint4& w1,
+                                          uint32_t d = 0u) {
+  hd = *reinterpret_cast<const uint4*>(p + (ul.o_hd + d));
+  w0 = *reinterpret_cast<const uint4*>(p + (ul.o_w0 + d));
+  w1 = *reinterpret_cast<const uint4*>(p + (ul.o_w1 + d));
 }
+// No extra row offset: the units of a ring share the UnitLane's row stride.
+struct NoRowDelta {
+  __device__ uint32_t operator()(int) const { return 0u; }
+};
 
 // The LDS operands of one unit against the activation groups gb .. gb+15 (image and scales in
 // LDS at smem): the A operands of its four MFMAs and the lane's two group-scale pairs.
@@ -249,13 +256,18 @@ template <int RING>
 struct UnitRegs {
   uint4 hd[RING], w0[RING], w1[RING];
 };
-template <int RING, class BaseFn>
-__device__ __forceinline__ void units_issue(UnitRegs<RING>& R, int nu, BaseFn base, const UnitLane& ul) {
+template <int RING, class BaseFn, class DFn = NoRowDelta>
+__device__ __forceinline__ void units_issue(UnitRegs<RING>& R, int nu, BaseFn base, const UnitLane& ul,
+                                            DFn dfn = DFn{}) {
 #pragma unroll
-  for (int r = 0; r < RING; ++r) unit_load(base(min(r, nu - 1)), ul, R.hd[r], R.w0[r], R.w1[r]);
+  for (int r = 0; r < RING; ++r) {
+    const int u = min(r, nu - 1);
+    unit_load(base(u), ul, R.hd[r], R.w0[r], R.w1[r], dfn(u));
+  }
 }
-template <bool STREAM, int RING, class BaseFn, class Proc>
-__device__ __forceinline__ void units_process(UnitRegs<RING>& R, int nu, BaseFn base, const UnitLane& ul, Proc proc) {
+template <bool STREAM, int RING, class BaseFn, class Proc, class DFn = NoRowDelta>
+__device__ __forceinline__ void units_process(UnitRegs<RING>& R, int nu, BaseFn base, const UnitLane& ul, Proc proc,
+                                              DFn dfn = DFn{}) {
   if (!STREAM) {
 #pragma unroll
     for (int r = 0; r < RING; ++r)
@@ -268,7 +280,8 @@ __device__ __forceinline__ void units_process(UnitRegs<RING>& R, int nu, BaseFn 
         // the refill stays after unit r: the loads are invariant, and the scheduler would
         // otherwise issue every refill first, with all their registers live at once
         __builtin_amdgcn_sched_barrier(0);
-        unit_load(base(min(u0 + r + RING, nu - 1)), ul, R.hd[r], R.w0[r], R.w1[r]);
+        const int un = min(u0 + r + RING, nu - 1);
+        unit_load(base(un), ul, R.hd[r], R.w0[r], R.w1[r], dfn(un));
       }
     }
   }
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
   constexpr bool STREAM = DN == 0;
   __shared__ __align__(16) uint8_t smem[kQ4Smem];
   __shared__ int sel_i[16];
-  __shared__ float sel_w[17];  // [k]: weight of the shared expert
+  __shared__ float sel_w[kQ4MaxSlots];  // [k ..]: weight of the shared expert (each of its slots)
   __shared__ int sel_o[16];
   __shared__ uint32_t sel_k[16];
   __shared__ uint32_t route_tmp[128];  // routing: compacted candidates
@@ -444,8 +457,11 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       const bool sh = slot >= a.k;
       const int mat = wave >> 1, kh = wave & 1;
       const int e = sh ? 0 : sel_i[slot];
-      const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) : expert_at(mat ? a.up : a.gate, e);
       const uint32_t rb = (uint32_t)nsbH * 144u;
+      // shared slot k + j: rows j*I .. j*I + I - 1 of the shared gate and up matrices (j > 0
+      // only in the streaming instantiation)
+      const uint8_t* W = sh ? (mat ? a.sh_up : a.sh_gate) + (STREAM ? (size_t)(slot - a.k) * a.I * rb : 0)
+                            : expert_at(mat ? a.up : a.gate, e);
       const int nlo = (nsbH + 1) >> 1;  // super-blocks of half 0 (half 1 takes the rest)
       const int c0 = kh ? nlo : 0, nu = kh ? nsbH - nlo : nlo;
       const uint8_t* Wr = uniform_ptr(W + (size_t)(urow * 16) * rb + (size_t)c0 * 144);
@@ -488,7 +504,8 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       }
       XTRACE(wave);  // per wave: dot products done
       acc = row_total(acc);
-      if (wave == 0 && a.has_sh && lane == 0) sel_w[a.k] = a.sh_gate_inp ? sigmoidf_(zsh) : 1.f;
+      if (wave == 0 && (STREAM ? lane < a.nsh : a.has_sh && lane == 0))
+        sel_w[a.k + (STREAM ? lane : 0)] = a.sh_gate_inp ? sigmoidf_(zsh) : 1.f;
       if (lane < 16) gu_part[mat][kh][lane] = acc;
       TRACE(3);
       __syncthreads();
@@ -536,6 +553,13 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
     TRACE(1);
     if (ok_flag) {
       const uint32_t rb = (uint32_t)nsbI * 144u;
+      // The shared expert's down rows are nsh times longer (sh_rb bytes apart); its slots take
+      // one column range each (the streaming instantiation alone runs nsh > 1): row i of a unit
+      // of a shared slot sits i * (sh_rb - rb) bytes further than the UnitLane's i * rb.
+      const uint32_t sh_rb = rb * (uint32_t)max(a.nsh, 1);
+      const uint32_t dsh = (uint32_t)(lane & 15) * (sh_rb - rb);
+      const int ush0 = max(0, (a.k - wave + 3) >> 2) * nsbI;  // the wave's first unit of a shared slot
+      [[maybe_unused]] auto row_delta = [&](int u) { return u >= ush0 ? dsh : 0u; };
       const int nsw = (a.ktot - wave + 3) >> 2;  // slots of this wave: wave, wave + 4, ...
       const int nu = nsw * nsbI;                 // units: slot-major, super-blocks within
       const UnitLane ul = unit_lane(rb);
@@ -560,14 +584,16 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         // ends the slot (bits 0-15, 16-20, 31)
         if (nu > 0) {
           const int u = min(lane, nu - 1), j = u / nsbI, c = u - j * nsbI, s = wave + 4 * j;
-          const uint8_t* D = s >= a.k ? a.sh_down : expert_at(a.down, sel_i[min(s, a.k - 1)]);
+          // shared slot k + j': columns j'*I .. of the shared down rows, which are nsh times longer
+          const uint8_t* D = s >= a.k ? a.sh_down + (size_t)(s - a.k) * rb + (size_t)(q * 16) * sh_rb
+                                      : expert_at(a.down, sel_i[min(s, a.k - 1)]) + (size_t)(q * 16) * rb;
           if (lane < kQ4MaxUnitsD) {
-            dn_tab[wave][lane] = D + (size_t)(q * 16) * rb + (size_t)c * 144;
+            dn_tab[wave][lane] = D + (size_t)c * 144;
             dn_grp[wave][lane] = (uint32_t)(s * nGI + c * 16) | ((uint32_t)s << 16) | (c == nsbI - 1 ? 0x80000000u : 0u);
           }
           lds_drain();
           __builtin_amdgcn_wave_barrier();
-          units_issue(R, nu, [&](int u) { return uniform_ptr(dn_tab[wave][u]); }, ul);
+          units_issue(R, nu, [&](int u) { return uniform_ptr(dn_tab[wave][u]); }, ul, row_delta);
         }
       }
       if (wave == 0) route_finish(rc, rs, sel_w, sel_o);  // wave 0 alone uses weights and order
@@ -649,7 +675,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
                                     if (lane < 16) dn_part[(gw >> 16) & 31u][lane] = acc;
                                     acc = 0.f;
                                   }
-                                });
+                                }, row_delta);
         }
         XTRACE(wave);  // per wave: dot products done
         __syncthreads();
@@ -658,7 +684,12 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
           float yv = 0.f;  // routed slots in ascending expert order (layer.rs:1092-1106)
           for (int p = 0; p < a.k; ++p) yv = yv + dn_part[sel_o[p]][tid];
           yv = yv + ybias;
-          if (a.has_sh) yv = yv + dn_part[a.k][tid];  // shared expert after the routed sum
+          if (a.has_sh) {  // shared expert after the routed sum, its slots in column order
+            float ysh = dn_part[a.k][tid];
+            if constexpr (STREAM)
+              for (int s2 = 1; s2 < a.nsh; ++s2) ysh = ysh + dn_part[a.k + s2][tid];
+            yv = yv + ysh;
+          }
           if (NORM) yv = yres + yv;  // hidden = residual + moe_out (layer.rs:473)
           a.y[rr] = yv;
         }
@@ -685,8 +716,10 @@ struct Q4Grid {
 };
 // Roles of a launch: gt row tiles per gate/up workgroup, the fewest (1, 2 or 4) that keep the
 // grid within 3 workgroups per CU.
+// Slots of the shared expert: Ish / I column ranges of I (0 without one).
+uint64_t q4_nsh(const mr_layer& L) { return L.d.sh_gate ? L.Ish / L.I : 0u; }
 Q4Grid q4_grid(const mr_layer& L, int n_cu) {
-  const uint64_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + has_sh, nGI = L.I / 16;
+  const uint64_t has_sh = L.d.sh_gate ? 1u : 0u, ktot = L.d.top_k + q4_nsh(L), nGI = L.I / 16;
   const uint64_t R = (L.E + has_sh + 3) / 4, ND = L.H / 16;
   const uint64_t cap = std::min<uint64_t>(3ull * (uint64_t)n_cu, (uint64_t)kMaxGrid);
   uint64_t gt = 1;
@@ -696,15 +729,15 @@ Q4Grid q4_grid(const mr_layer& L, int n_cu) {
 // Units of the busiest gate/up and down waves.
 uint64_t q4_units_gu(const mr_layer& L) { return (L.H / 256 + 1) / 2; }
 uint64_t q4_units_dn(const mr_layer& L) {
-  const uint64_t ktot = L.d.top_k + (L.d.sh_gate ? 1u : 0u);
+  const uint64_t ktot = L.d.top_k + q4_nsh(L);
   return (ktot + 3) / 4 * (L.I / 256);
 }
 // The instantiation for a shape: DN = I/256 when every wave's units fit its registers
 // (I <= 768, H <= 2048, the down waves' slots within kQ4RingD / DN, one row tile per gate/up
-// workgroup), else 0 (streaming).
+// workgroup, a shared expert no wider than the routed ones), else 0 (streaming).
 int q4_dn(const mr_layer& L, int n_cu) {
-  const uint64_t dn = L.I / 256, ktot = L.d.top_k + (L.d.sh_gate ? 1u : 0u);
-  if (dn >= 1 && dn <= 3 && q4_units_gu(L) <= (uint64_t)kQ4RingG && (ktot + 3) / 4 <= (uint64_t)(kQ4RingD / dn) &&
+  const uint64_t dn = L.I / 256, ktot = L.d.top_k + q4_nsh(L);
+  if (dn >= 1 && dn <= 3 && q4_nsh(L) <= 1 && q4_units_gu(L) <= (uint64_t)kQ4RingG && (ktot + 3) / 4 <= (uint64_t)(kQ4RingD / dn) &&
       q4_grid(L, n_cu).gt == 1)
     return (int)dn;
   return 0;
@@ -726,9 +759,9 @@ bool fused_q4k_supported(const mr_layer& L, int n_cu) {
   if (L.H > (uint32_t)kQ4MaxH || L.I > (uint32_t)kQ4MaxI) return false;
   const uint32_t has_sh = L.d.sh_gate ? 1u : 0u;
   if (has_sh && (L.d.sh_gate->type != MR_GGML_Q4_K || L.d.sh_up->type != MR_GGML_Q4_K ||
-                 L.d.sh_down->type != MR_GGML_Q4_K || L.Ish != L.I))
-    return false;
-  const uint64_t ktot = L.d.top_k + has_sh;
+                 L.d.sh_down->type != MR_GGML_Q4_K || L.Ish % L.I != 0))
+    return false;  // a shared expert as nsh = Ish / I slots of the routed width
+  const uint64_t ktot = L.d.top_k + q4_nsh(L);
   if (L.d.top_k > 16 || ktot > (uint64_t)kQ4MaxSlots || L.E > 512 || L.E + has_sh > (uint32_t)kMaxLogits) return false;
   if (ktot * L.I > (uint64_t)kQ4MaxKI) return false;  // the down input image of every slot in LDS
   if (q4_units_dn(L) > (uint64_t)kQ4MaxUnitsD) return false;  // the down waves' unit tables
@@ -777,7 +810,8 @@ hipError_t launch_fused_q4k(const Launch& K, const mr_layer& L, const float* x, 
   a.sh_gate_inp = L.d.sh_gate_inp;
   a.x = x, a.y = y, a.fs = L.fused_sync, a.err = err;
   a.logits_out = L.logits_out;
-  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)L.d.top_k, a.ktot = a.k + a.has_sh;
+  a.nsh = (int)q4_nsh(L);
+  a.H = (int)L.H, a.I = (int)L.I, a.E = (int)L.E, a.k = (int)L.d.top_k, a.ktot = a.k + a.nsh;
   const uint64_t nGI = L.I / 16;
   a.himg = reinterpret_cast<uint32_t*>(img_base);
   a.hsc = reinterpret_cast<float*>(img_base + (uint64_t)a.ktot * nGI * 32);

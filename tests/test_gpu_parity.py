@@ -141,10 +141,20 @@ WIDE_SH = {
     "mxfp4-k8-shared-2944": W.LayerSpec(223, 0, W.GGML_MXFP4, 2048, 384, 64, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU,
                                         False, False, sh_inter=2944, sh_type=W.GGML_MXFP4),
 }
+# Q4_K shared experts wider than the routed experts: the fused decode kernel runs the shared
+# expert as Ish / I slots of the routed width (gate/up rows and down columns j*I .. j*I + I - 1
+# of slot j, added in column order after the routed sum), in its streaming instantiation.
+WIDE_SH_Q4 = {
+    "q4k-k4-shared-x4": W.LayerSpec(224, 0, W.GGML_Q4_K, 512, 256, 16, 4, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                    False, False, sh_inter=1024),
+    "q4k-k8-shared-x3-H2048": W.LayerSpec(225, 0, W.GGML_Q4_K, 2048, 512, 64, 8, W.ROUTE_NORM_TOPK, W.ACT_SILU,
+                                          False, False, sh_inter=1536),
+}
 SPECS = {
     **WIDE_Q4,
     **WIDE_MX,
     **WIDE_SH,
+    **WIDE_SH_Q4,
     "tiny-mxfp4": TINY_MX,
     "tiny-q4k-plain": TINY_Q4P,
     "tiny-q4k": TINY_Q4,
@@ -443,7 +453,8 @@ def test_batched_graph_replay_matches_eager(gpu_ctx, layers):
 # ---- fused single-launch decode kernels (MXFP4 and Q4_K) ------------------------------
 
 FUSED = ["tiny-mxfp4", "C1-gpt-oss", "tiny-q4k", "tiny-q4k-plain", "tiny-q4k-shared", "C3-qwen3-layer0",
-         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4, *WIDE_MX, *WIDE_SH, "tiny-mxfp4-k10"]
+         "C4-coder-next-layer0", *C4_RANGE, *WIDE_Q4, *WIDE_MX, *WIDE_SH, *WIDE_SH_Q4,
+         "tiny-mxfp4-k10"]
 
 
 @pytest.mark.parametrize("name", FUSED)
